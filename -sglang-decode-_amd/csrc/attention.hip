@@ -1,0 +1,51 @@
+// sgd_persistent_decode: host-side validation of one attention launch and the
+// choice of kernel.  Geometry and layout checks happen here, before any launch,
+// so a bad argument is an SGD_EINVAL and never a device fault.
+#include "attention_common.h"
+
+namespace sgd {
+int launch_attention_generic(const sgd_decode_args &a, bool vec, hipStream_t stream);
+}
+
+using namespace sgd;
+
+namespace {
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// 16-byte vector loads need unit head_dim stride and 16-byte aligned rows.
+bool vector_layout(const sgd_decode_args &a) {
+    if (a.k_stride[3] != 1 || a.v_stride[3] != 1) return false;
+    if (!aligned16(a.k) || !aligned16(a.v)) return false;
+    for (int i = 0; i < 3; ++i)
+        if (a.k_stride[i] % 8 != 0 || a.v_stride[i] % 8 != 0) return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" int sgd_persistent_decode(const sgd_decode_args *args, void *stream) {
+    if (!args) return einval("persistent_decode: null args");
+    const sgd_decode_args &a = *args;
+    if (a.kv_heads <= 0 || a.query_heads <= 0 || a.query_heads % a.kv_heads != 0)
+        return einval("persistent_decode: heads %d/%d", a.query_heads, a.kv_heads);
+    const int g = a.query_heads / a.kv_heads;
+    if (g != 1 && g != 2 && g != 4 && g != 8 && g != 16) return einval("persistent_decode: group %d", g);
+    if (a.head_dim != 64 && a.head_dim != 128 && a.head_dim != 256)
+        return einval("persistent_decode: head_dim %d", a.head_dim);
+    if (a.dtype != SGD_BF16 && a.dtype != SGD_FP16) return einval("persistent_decode: dtype %d", a.dtype);
+    if (a.workers <= 0 || a.max_splits <= 0 || a.page_size <= 0)
+        return einval("persistent_decode: workers/max_splits/page_size");
+    if (a.csr && (a.page_size != 1 || !a.indptr)) return einval("persistent_decode: CSR needs page_size 1 + indptr");
+    if (!a.q || !a.k || !a.v || !a.pages || !a.partial || !a.lse || !a.counter)
+        return einval("persistent_decode: null buffer");
+    const bool vec = vector_layout(a);
+    clear_stale_error();
+    switch (a.kernel) {
+        case SGD_KERNEL_AUTO:
+        case SGD_KERNEL_GENERIC:
+            return launch_attention_generic(a, vec, (hipStream_t)stream);
+        default:
+            return einval("persistent_decode: kernel %d not available", a.kernel);
+    }
+}

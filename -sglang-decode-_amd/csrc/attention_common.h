@@ -1,0 +1,98 @@
+// Task decode and persistent dispatch shared by every attention kernel.
+//
+// A worker is one workgroup.  Its task stream follows the plan's mode exactly as
+// kernels/attention.py:87-130: D1/D4 claim pack indices from the per-layer
+// counter (one relaxed atomic per claim, :103-106 and :125-126), STATIC walks the
+// worker's linked list (:107-109, :127-128), R0/R1 stride by the worker count
+// (:110-112, :129-130).  Tasks are (record, kv head) = (task / Hkv, task % Hkv);
+// R0 recovers the request by an upper-bound search of the request offsets
+// (:25-39), the other modes read the SoA record, through the bucket order except
+// in STATIC mode (:41-47).
+#pragma once
+
+#include "common.h"
+
+namespace sgd {
+
+struct TaskInfo {
+    int32_t request, split, start, end, group;
+};
+
+__device__ __forceinline__ TaskInfo decode_task(const sgd_decode_args &a, int32_t task, int32_t mode) {
+    TaskInfo t;
+    const int32_t hkv = a.kv_heads;
+    t.group = task % hkv;
+    int32_t rec = task / hkv;
+    if (mode == 0) {
+        int32_t lo = 0, hi = *a.active;
+        while (lo < hi) {
+            const int32_t mid = (lo + hi) >> 1;
+            if (rec >= a.offsets[mid + 1]) lo = mid + 1;
+            else hi = mid;
+        }
+        t.request = lo;
+        t.split = rec - a.offsets[lo];
+        const int32_t c = a.chunk[lo];
+        t.start = t.split * c;
+        t.end = min(t.start + c, a.lengths[lo]);
+    } else {
+        if (mode != 2) rec = a.order[rec];
+        t.request = a.request[rec];
+        t.split = a.split[rec];
+        t.start = a.begin[rec];
+        t.end = a.end[rec];
+    }
+    return t;
+}
+
+// Orders LDS traffic between lanes of ONE wave without a workgroup barrier.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Runs `run(task, mode)` for every task of this worker.  All threads of the
+// workgroup execute it uniformly; `sh_cursor` is one int of LDS.
+template <class Run>
+__device__ void for_each_task(const sgd_decode_args &a, int32_t *sh_cursor, Run &&run) {
+    const int32_t worker = blockIdx.x;
+    const int32_t mode = *a.mode;
+    const int32_t total = *a.record_count * a.kv_heads;
+    const bool dynamic = mode >= 3;
+    int32_t cursor, limit;
+    if (dynamic) {
+        if (threadIdx.x == 0) *sh_cursor = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED,
+                                                                  __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        cursor = *sh_cursor;
+        limit = *a.num_packs;
+    } else if (mode == 2) {
+        cursor = a.static_head[worker];
+        limit = total;
+    } else {
+        cursor = worker;
+        limit = total;
+    }
+    while (cursor >= 0 && cursor < limit) {
+        int32_t first = cursor, count = 1;
+        if (dynamic) {
+            first = a.pack_first[cursor];
+            count = a.pack_count[cursor];
+        }
+        for (int32_t i = 0; i < count; ++i) run(first + i, mode);
+        if (dynamic) {
+            __syncthreads();
+            if (threadIdx.x == 0) *sh_cursor = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED,
+                                                                      __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            cursor = *sh_cursor;
+        } else if (mode == 2) {
+            cursor = a.static_next[cursor];
+        } else {
+            cursor += a.workers;
+        }
+    }
+}
+
+}  // namespace sgd

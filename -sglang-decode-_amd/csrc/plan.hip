@@ -1,0 +1,466 @@
+// Device plan construction for the persistent decode: count/scan, SoA records,
+// mode selection + bucket order + packs, and the STATIC (LPT) lists.
+//
+// Every stage runs in ONE 1024-thread workgroup: the batch (<= 4096 rows) and the
+// record table (<= 16384 records) are small, and keeping the whole plan in one
+// workgroup lets the fused entry run all stages in a single launch with only
+// workgroup barriers between them (the reference launches four kernels,
+// planning/builder.py:6-28).  Results are identical to the reference stages:
+//   count_scan           kernels/plan.py:7-27
+//   emit_records         kernels/plan.py:30-45
+//   make_order_and_packs kernels/plan.py:48-100
+//   greedy_lists         kernels/plan.py:103-135 (same lists as planning/reference.py:57-67)
+// Integer arithmetic is int32 with wrap-around, like the reference's lanes.
+#include "common.h"
+
+namespace sgd {
+namespace {
+
+constexpr int kPlanThreads = 1024;
+constexpr int kMaxBuckets = 16;
+
+__device__ __forceinline__ int32_t wadd(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+__device__ __forceinline__ int32_t wmul(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
+__device__ __forceinline__ int32_t cdiv(int32_t a, int32_t b) { return wadd(wadd(a, b), -1) / b; }
+
+struct PlanShared {
+    int32_t scan_tmp[16];
+    uint64_t scan_tmp64[16];
+    int32_t bucket_size[kMaxBuckets];
+    int32_t bucket_record_base[kMaxBuckets];
+    int32_t bucket_pack_base[kMaxBuckets];
+    int32_t bucket_pack_count[kMaxBuckets];
+    int32_t bucket_width[kMaxBuckets];
+    int32_t bucket_packed_packs[kMaxBuckets];
+    int32_t bucket_packed_tasks[kMaxBuckets];
+    int32_t mode;
+    int32_t max_w, min_w;
+    int32_t red_max[16], red_min[16];
+};
+
+// ---------------------------------------------------------------- count/scan
+__device__ void stage_count_scan(const int32_t *lengths, const int32_t *splits, const int32_t *active_p,
+                                 int32_t *counts, int32_t *offsets, int32_t *chunk, int32_t *record_count,
+                                 int32_t *error, int32_t bcap, int32_t smax, int32_t max_context,
+                                 PlanShared &sh) {
+    const int tid = threadIdx.x;
+    const int per = (bcap + kPlanThreads - 1) / kPlanThreads;  // rows per thread (contiguous)
+    const int32_t active = *active_p;
+    const int r0 = tid * per;
+    int invalid_any = 0;
+    int32_t local = 0;
+    // pass 1: validity, chunk, n
+    for (int i = 0; i < per; ++i) {
+        const int r = r0 + i;
+        if (r >= bcap) break;
+        const bool live = r < active;
+        const int32_t length = live ? lengths[r] : 0;
+        const int32_t s = live ? splits[r] : 1;
+        const bool invalid = live && (length < 0 || length > max_context || s < 1 || s > smax);
+        invalid_any |= invalid;
+        const int32_t c = wmul(cdiv(cdiv(max(length, 0), max(s, 1)), 32), 32);
+        chunk[r] = c;
+        const int32_t n = (live && !invalid) ? cdiv(length, max(c, 1)) : 0;
+        counts[r] = n;  // provisional; rewritten below if the batch is in error
+        local = wadd(local, n);
+    }
+    const bool err = (active < 0) || (active > bcap) || __syncthreads_or(invalid_any);
+    if (err) local = 0;
+    int32_t total;
+    int32_t running = block_exclusive_scan<int32_t>(local, sh.scan_tmp, &total);
+    for (int i = 0; i < per; ++i) {
+        const int r = r0 + i;
+        if (r >= bcap) break;
+        const int32_t n = err ? 0 : counts[r];
+        counts[r] = n;
+        offsets[r] = running;
+        running = wadd(running, n);
+    }
+    if (tid == 0) {
+        offsets[bcap] = total;
+        *record_count = total;
+        *error = err ? 1 : 0;
+    }
+}
+
+// ---------------------------------------------------------------- records
+__device__ void stage_emit_records(const int32_t *lengths, const int32_t *counts, const int32_t *offsets,
+                                   const int32_t *chunk, int32_t *request, int32_t *split, int32_t *begin,
+                                   int32_t *end, int32_t *weight, int32_t bcap, int32_t smax,
+                                   int32_t block_kv) {
+    const int64_t pairs = (int64_t)bcap * smax;
+    for (int64_t p = threadIdx.x; p < pairs; p += kPlanThreads) {
+        const int r = (int)(p / smax), s = (int)(p % smax);
+        const int32_t n = counts[r];
+        if (s >= n) continue;
+        const int32_t idx = wadd(offsets[r], s);
+        const int32_t c = chunk[r];
+        const int32_t b = wmul(s, c);
+        const int32_t e = min(wadd(b, c), lengths[r]);
+        request[idx] = r;
+        split[idx] = s;
+        begin[idx] = b;
+        end[idx] = e;
+        weight[idx] = cdiv(wadd(e, -b), block_kv);
+    }
+}
+
+__device__ __forceinline__ int bucket_of(int32_t w, int buckets) {
+    int b = 0;
+    for (int k = 1; k < buckets; ++k) b += w > (1 << (k - 1));
+    return b;
+}
+
+// ---------------------------------------------------------------- mode, order, packs
+__device__ void stage_order_and_packs(const int32_t *weight, const int32_t *record_count, int32_t *order,
+                                      int32_t *pack_first, int32_t *pack_count, int32_t *num_packs,
+                                      int32_t *mode_out, const int32_t *rules, int32_t rule_count,
+                                      int32_t force, int32_t hkv, int32_t workers, int32_t buckets,
+                                      int32_t record_capacity, PlanShared &sh) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int32_t total = *record_count;
+    const int per = (record_capacity + kPlanThreads - 1) / kPlanThreads;
+    const int i0 = tid * per;
+    // max/min weight over valid records (max starts at 1, min at INT32_MAX as plan.py:57-58)
+    int32_t mx = 1, mn = INT32_MAX;
+    for (int k = 0; k < per; ++k) {
+        const int i = i0 + k;
+        if (i >= total) break;
+        const int32_t w = weight[i];
+        mx = max(mx, w);
+        mn = min(mn, w);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        mx = max(mx, __shfl_xor(mx, o, 64));
+        mn = min(mn, __shfl_xor(mn, o, 64));
+    }
+    if (lane == 0) { sh.red_max[wid] = mx; sh.red_min[wid] = mn; }
+    __syncthreads();
+    if (tid == 0) {
+        int32_t a = 1, b = INT32_MAX;
+        for (int w = 0; w < kPlanThreads / 64; ++w) { a = max(a, sh.red_max[w]); b = min(b, sh.red_min[w]); }
+        const int32_t ratio = wmul(a, 100) / max(b, 1);
+        const int32_t tasks = wmul(total, hkv);
+        int32_t mode = 1;
+        for (int row = 0; row < rule_count; ++row) {
+            const int32_t *r = rules + 5 * row;
+            if (tasks >= r[0] && tasks <= r[1] && ratio >= r[2] && ratio <= r[3]) mode = r[4];
+        }
+        if (a == b) mode = 1;
+        if (force >= 0) mode = force;
+        sh.mode = mode;
+        sh.max_w = a;
+        *mode_out = mode;
+    }
+    __syncthreads();
+    const int32_t mode = sh.mode, max_w = sh.max_w;
+    if (mode == 0 || mode == 1) {
+        for (int i = tid; i < total; i += kPlanThreads) order[i] = i;
+        if (tid == 0) *num_packs = 0;
+        return;
+    }
+    // Stable partition by bucket, heaviest first.  Each thread owns a contiguous
+    // segment; per-bucket counts are packed 4 x 16-bit per uint64 so four block
+    // scans cover 16 buckets (segment counts <= 16, totals <= 16384 < 2^16).
+    uint64_t cnt[4] = {0, 0, 0, 0};
+    for (int k = 0; k < per; ++k) {
+        const int i = i0 + k;
+        if (i >= total) break;
+        const int b = bucket_of(weight[i], buckets);
+        cnt[b >> 2] += (uint64_t)1 << (16 * (b & 3));
+    }
+    uint64_t base[4], tot[4];
+    for (int q = 0; q < 4; ++q) base[q] = block_exclusive_scan<uint64_t>(cnt[q], sh.scan_tmp64, &tot[q]);
+    if (tid == 0) {
+        int32_t rec_base = 0, pack_base = 0;
+        for (int b = buckets - 1; b >= 0; --b) {
+            const int32_t size = (int32_t)((tot[b >> 2] >> (16 * (b & 3))) & 0xffff);
+            const int32_t tasks = size * hkv;
+            const int32_t width = (mode == 4) ? min(4, max(1, max_w / (1 << b))) : 1;
+            const int32_t packed_tasks = max(0, tasks - workers) / width * width;
+            const int32_t packed_packs = packed_tasks / width;
+            const int32_t count = packed_packs + tasks - packed_tasks;
+            sh.bucket_size[b] = size;
+            sh.bucket_record_base[b] = rec_base;
+            sh.bucket_pack_base[b] = pack_base;
+            sh.bucket_pack_count[b] = count;
+            sh.bucket_width[b] = width;
+            sh.bucket_packed_packs[b] = packed_packs;
+            sh.bucket_packed_tasks[b] = packed_tasks;
+            rec_base += size;
+            pack_base += count;
+        }
+        *num_packs = pack_base;
+    }
+    __syncthreads();
+    int32_t rank[kMaxBuckets];
+    for (int b = 0; b < kMaxBuckets; ++b) rank[b] = (int32_t)((base[b >> 2] >> (16 * (b & 3))) & 0xffff);
+    for (int k = 0; k < per; ++k) {
+        const int i = i0 + k;
+        if (i >= total) break;
+        const int b = bucket_of(weight[i], buckets);
+        int32_t r = 0;
+#pragma unroll
+        for (int q = 0; q < kMaxBuckets; ++q)
+            if (q == b) { r = rank[q]; rank[q] = r + 1; }
+        order[sh.bucket_record_base[b] + r] = i;
+    }
+    for (int b = buckets - 1; b >= 0; --b) {
+        const int32_t count = sh.bucket_pack_count[b], width = sh.bucket_width[b];
+        const int32_t pp = sh.bucket_packed_packs[b], pt = sh.bucket_packed_tasks[b];
+        const int32_t first0 = sh.bucket_record_base[b] * hkv, out0 = sh.bucket_pack_base[b];
+        for (int p = tid; p < count; p += kPlanThreads) {
+            const bool packed = p < pp;
+            pack_first[out0 + p] = first0 + (packed ? p * width : pt + p - pp);
+            pack_count[out0 + p] = packed ? width : 1;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- STATIC lists
+// Longest-processing-time assignment: records in (-weight, record) order, each
+// record's kv_heads tasks in task order, each task to the worker with the least
+// (load, worker).  Records are sorted once (bitonic, in LDS); the assignment loop
+// runs on wave 0 with every lane caching the minimum of its share of workers.
+constexpr int kGreedyMaxRecords = 16384;
+constexpr int kGreedyMaxWorkers = 4096;
+
+struct GreedyShared {
+    uint32_t keys[kGreedyMaxRecords];     // (0xffff - weight) << 16 | record, sorted ascending
+    int32_t load[kGreedyMaxWorkers];
+    int32_t tail[kGreedyMaxWorkers];
+};
+
+__device__ void stage_greedy_lists(const int32_t *weight, const int32_t *record_count, const int32_t *mode_p,
+                                   int32_t *static_head, int32_t *static_next, int32_t hkv,
+                                   int32_t workers, GreedyShared &g) {
+    if (*mode_p != 2) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int32_t total = *record_count;
+    int n2 = 1;
+    while (n2 < total) n2 <<= 1;
+    for (int i = tid; i < n2; i += kPlanThreads)
+        g.keys[i] = i < total ? ((uint32_t)(0xffff - weight[i]) << 16) | (uint32_t)i : 0xffffffffu;
+    for (int w = tid; w < workers; w += kPlanThreads) {
+        g.load[w] = 0;
+        g.tail[w] = -1;
+        static_head[w] = -1;
+    }
+    __syncthreads();
+    for (int k = 2; k <= n2; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < n2; i += kPlanThreads) {
+                const int p = i ^ j;
+                if (p > i) {
+                    const uint32_t a = g.keys[i], b = g.keys[p];
+                    const bool up = (i & k) == 0;
+                    if ((a > b) == up) { g.keys[i] = b; g.keys[p] = a; }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (tid >= 64) return;
+    // lane l owns workers l, l+64, ...; cache (load << 32 | worker) of its minimum.
+    auto local_min = [&]() {
+        uint64_t best = ~0ull;
+        for (int w = lane; w < workers; w += 64) {
+            const uint64_t key = ((uint64_t)(uint32_t)g.load[w] << 32) | (uint32_t)w;
+            best = key < best ? key : best;
+        }
+        return best;
+    };
+    uint64_t mine = local_min();
+    for (int r = 0; r < total; ++r) {
+        const uint32_t key = g.keys[r];
+        const int32_t rec = (int32_t)(key & 0xffff);
+        const int32_t w = 0xffff - (int32_t)(key >> 16);
+        for (int h = 0; h < hkv; ++h) {
+            uint64_t best = mine;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const uint64_t other = __shfl_xor(best, o, 64);
+                best = other < best ? other : best;
+            }
+            const int owner = (int)(best & 0xffffffffu);
+            const int32_t task = rec * hkv + h;
+            if (lane == (owner & 63)) {
+                const int32_t t = g.tail[owner];
+                if (t < 0) static_head[owner] = task;
+                else static_next[t] = task;
+                static_next[task] = -1;
+                g.tail[owner] = task;
+                g.load[owner] += w;
+                mine = local_min();
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- kernels
+__global__ __launch_bounds__(kPlanThreads) void k_count_scan(const int32_t *lengths, const int32_t *splits,
+                                                             const int32_t *active, int32_t *counts,
+                                                             int32_t *offsets, int32_t *chunk,
+                                                             int32_t *record_count, int32_t *error,
+                                                             int32_t bcap, int32_t smax, int32_t max_context) {
+    __shared__ PlanShared sh;
+    stage_count_scan(lengths, splits, active, counts, offsets, chunk, record_count, error, bcap, smax,
+                     max_context, sh);
+}
+
+__global__ __launch_bounds__(kPlanThreads) void k_emit_records(const int32_t *lengths, const int32_t *counts,
+                                                               const int32_t *offsets, const int32_t *chunk,
+                                                               int32_t *request, int32_t *split, int32_t *begin,
+                                                               int32_t *end, int32_t *weight, int32_t bcap,
+                                                               int32_t smax, int32_t block_kv) {
+    stage_emit_records(lengths, counts, offsets, chunk, request, split, begin, end, weight, bcap, smax,
+                       block_kv);
+}
+
+__global__ __launch_bounds__(kPlanThreads) void k_order_and_packs(
+    const int32_t *weight, const int32_t *record_count, int32_t *order, int32_t *pack_first,
+    int32_t *pack_count, int32_t *num_packs, int32_t *mode, const int32_t *rules, int32_t rule_count,
+    int32_t force, int32_t hkv, int32_t workers, int32_t buckets, int32_t record_capacity) {
+    __shared__ PlanShared sh;
+    stage_order_and_packs(weight, record_count, order, pack_first, pack_count, num_packs, mode, rules,
+                          rule_count, force, hkv, workers, buckets, record_capacity, sh);
+}
+
+__global__ __launch_bounds__(kPlanThreads) void k_greedy_lists(const int32_t *weight, const int32_t *record_count,
+                                                               const int32_t *mode, int32_t *static_head,
+                                                               int32_t *static_next, int32_t hkv,
+                                                               int32_t workers) {
+    extern __shared__ char dyn[];
+    stage_greedy_lists(weight, record_count, mode, static_head, static_next, hkv, workers,
+                       *reinterpret_cast<GreedyShared *>(dyn));
+}
+
+__global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p, int32_t force, int32_t run_greedy,
+                                                             int32_t *zero_counters, int32_t num_counters) {
+    __shared__ PlanShared sh;
+    extern __shared__ char dyn[];
+    for (int i = threadIdx.x; i < num_counters; i += kPlanThreads) zero_counters[i] = 0;
+    stage_count_scan(p.lengths, p.splits, p.active, p.counts, p.offsets, p.chunk, p.record_count, p.error,
+                     p.batch_capacity, p.max_splits, p.max_context, sh);
+    if (force == 0) {  // forced R0: counts/offsets only (planning/builder.py:11-14)
+        if (threadIdx.x == 0) { *p.mode = 0; *p.num_packs = 0; }
+        return;
+    }
+    __syncthreads();
+    stage_emit_records(p.lengths, p.counts, p.offsets, p.chunk, p.request, p.split, p.begin, p.end, p.weight,
+                       p.batch_capacity, p.max_splits, p.block_kv);
+    __syncthreads();
+    stage_order_and_packs(p.weight, p.record_count, p.order, p.pack_first, p.pack_count, p.num_packs, p.mode,
+                          p.rules, p.rule_count, force, p.kv_heads, p.workers, p.buckets,
+                          p.batch_capacity * p.max_splits, sh);
+    if (run_greedy) {
+        __syncthreads();
+        stage_greedy_lists(p.weight, p.record_count, p.mode, p.static_head, p.static_next, p.kv_heads,
+                           p.workers, *reinterpret_cast<GreedyShared *>(dyn));
+    }
+}
+
+size_t greedy_shared_bytes(int32_t record_capacity, int32_t workers) {
+    (void)record_capacity;
+    (void)workers;
+    return sizeof(GreedyShared);
+}
+
+bool greedy_attr_set = false;
+
+int prepare_greedy_launch() {
+    if (greedy_attr_set) return 0;
+    const int bytes = (int)sizeof(GreedyShared);
+    if (hipFuncSetAttribute((const void *)k_greedy_lists, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) !=
+            hipSuccess ||
+        hipFuncSetAttribute((const void *)k_build_plan, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) !=
+            hipSuccess)
+        return einval("hipFuncSetAttribute(max dynamic LDS %d) failed", bytes);
+    greedy_attr_set = true;
+    return 0;
+}
+
+int check_plan_geometry(int32_t bcap, int32_t smax, int32_t hkv, int32_t workers, int32_t buckets) {
+    if (bcap <= 0 || bcap > 4096) return einval("batch_capacity %d outside [1, 4096]", bcap);
+    if (smax <= 0 || (int64_t)bcap * smax > kGreedyMaxRecords)
+        return einval("record capacity %lld outside [1, %d]", (long long)bcap * smax, kGreedyMaxRecords);
+    if (hkv <= 0 || (int64_t)bcap * smax * hkv >= (1ll << 31)) return einval("task capacity overflow");
+    if (workers <= 0 || workers > kGreedyMaxWorkers) return einval("workers %d outside [1, %d]", workers,
+                                                                     kGreedyMaxWorkers);
+    if (buckets <= 0 || buckets > kMaxBuckets) return einval("buckets %d outside [1, %d]", buckets, kMaxBuckets);
+    return 0;
+}
+
+}  // namespace
+}  // namespace sgd
+
+using namespace sgd;
+
+extern "C" int sgd_count_scan(const int32_t *lengths, const int32_t *splits, const int32_t *active,
+                              int32_t *counts, int32_t *offsets, int32_t *chunk, int32_t *record_count,
+                              int32_t *error, int32_t bcap, int32_t smax, int32_t max_context, void *stream) {
+    if (bcap <= 0 || bcap > 4096 || smax <= 0) return einval("count_scan: bcap %d / smax %d", bcap, smax);
+    clear_stale_error();
+    hipLaunchKernelGGL(k_count_scan, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, lengths, splits,
+                       active, counts, offsets, chunk, record_count, error, bcap, smax, max_context);
+    return launch_status("count_scan");
+}
+
+extern "C" int sgd_emit_records(const int32_t *lengths, const int32_t *counts, const int32_t *offsets,
+                                const int32_t *chunk, int32_t *request, int32_t *split, int32_t *begin,
+                                int32_t *end, int32_t *weight, int32_t bcap, int32_t smax, int32_t block_kv,
+                                void *stream) {
+    if (bcap <= 0 || smax <= 0 || block_kv <= 0) return einval("emit_records: bad geometry");
+    clear_stale_error();
+    hipLaunchKernelGGL(k_emit_records, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, lengths, counts,
+                       offsets, chunk, request, split, begin, end, weight, bcap, smax, block_kv);
+    return launch_status("emit_records");
+}
+
+extern "C" int sgd_order_and_packs(const int32_t *weight, const int32_t *record_count, int32_t *order,
+                                   int32_t *pack_first, int32_t *pack_count, int32_t *num_packs, int32_t *mode,
+                                   const int32_t *rules, int32_t rule_count, int32_t force_mode,
+                                   int32_t kv_heads, int32_t workers, int32_t buckets,
+                                   int32_t record_capacity, void *stream) {
+    if (record_capacity <= 0 || record_capacity > kGreedyMaxRecords || kv_heads <= 0 || workers <= 0 ||
+        buckets <= 0 || buckets > kMaxBuckets || rule_count < 0)
+        return einval("order_and_packs: bad geometry");
+    clear_stale_error();
+    hipLaunchKernelGGL(k_order_and_packs, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, weight,
+                       record_count, order, pack_first, pack_count, num_packs, mode, rules, rule_count,
+                       force_mode, kv_heads, workers, buckets, record_capacity);
+    return launch_status("order_and_packs");
+}
+
+extern "C" int sgd_greedy_lists(const int32_t *weight, const int32_t *record_count, const int32_t *mode,
+                                int32_t *static_head, int32_t *static_next, int32_t kv_heads, int32_t workers,
+                                int32_t record_capacity, void *stream) {
+    if (record_capacity <= 0 || record_capacity > kGreedyMaxRecords || kv_heads <= 0 || workers <= 0 ||
+        workers > kGreedyMaxWorkers)
+        return einval("greedy_lists: bad geometry");
+    if (int rc = prepare_greedy_launch()) return rc;
+    clear_stale_error();
+    hipLaunchKernelGGL(k_greedy_lists, dim3(1), dim3(kPlanThreads), sizeof(GreedyShared), (hipStream_t)stream,
+                       weight, record_count, mode, static_head, static_next, kv_heads, workers);
+    return launch_status("greedy_lists");
+}
+
+extern "C" int sgd_build_plan(const sgd_plan_buffers *plan, int32_t force_mode, int32_t run_greedy,
+                              int32_t *zero_counters, int32_t num_counters, void *stream) {
+    if (!plan) return einval("build_plan: null plan");
+    if (int rc = check_plan_geometry(plan->batch_capacity, plan->max_splits, plan->kv_heads, plan->workers,
+                                     plan->buckets))
+        return rc;
+    if (plan->rule_count < 0) return einval("build_plan: negative rule_count");
+    if (num_counters < 0 || (num_counters > 0 && !zero_counters)) return einval("build_plan: counters");
+    size_t dyn = 0;
+    if (run_greedy) {
+        if (int rc = prepare_greedy_launch()) return rc;
+        dyn = sizeof(GreedyShared);
+    }
+    clear_stale_error();
+    hipLaunchKernelGGL(k_build_plan, dim3(1), dim3(kPlanThreads), dyn, (hipStream_t)stream, *plan, force_mode,
+                       run_greedy, zero_counters, num_counters);
+    return launch_status("build_plan");
+}

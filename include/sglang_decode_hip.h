@@ -1,0 +1,175 @@
+/*
+ * sglang_decode_hip.h -- C ABI of the MI355X (gfx950) persistent paged GQA
+ * decode-attention path.
+ *
+ * One entry per stage of the reference's launch sequence.  Each entry replaces
+ * a Triton `kernel[grid](...)` call of the reference (cited per entry, paths
+ * relative to the reference repository root) and is what its Python runtime
+ * binds through ctypes.
+ *
+ * Conventions
+ *   - Every pointer argument is a DEVICE pointer unless the comment says host.
+ *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream); every
+ *     entry enqueues on it and returns without synchronizing, so all entries are
+ *     capturable into a hipGraph.  No entry allocates, frees or reads device
+ *     memory from the host.
+ *   - Strides are int64 ELEMENT strides (torch's Tensor.stride()).
+ *   - Return value: 0 on success, SGD_EINVAL (-22) for arguments outside the
+ *     kernels' contract (checked on the host before any launch), otherwise the
+ *     hipError_t of the failed launch.  sgd_last_error() gives a message.
+ *   - Invalid DEVICE metadata (lengths/splits/active) is never an error code: the
+ *     plan sets error=1 and schedules no task, and the merge writes NaN.
+ */
+#ifndef SGLANG_DECODE_HIP_H
+#define SGLANG_DECODE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SGD_EINVAL (-22)
+
+enum sgd_dtype { SGD_BF16 = 0, SGD_FP16 = 1 };
+
+/* Attention kernel selection (sgd_decode_args.kernel). */
+enum sgd_kernel {
+    SGD_KERNEL_AUTO = 0,     /* pick by geometry: MFMA for group >= 8, VALU for group <= 4 */
+    SGD_KERNEL_GENERIC = 1,  /* any strides/alignment, any supported geometry */
+    SGD_KERNEL_VALU = 2,     /* LDS-staged K tile, wave64 DPP reductions, dot2 (group <= 4) */
+    SGD_KERNEL_MFMA = 3      /* MFMA QK^T and PV (group >= 8) */
+};
+
+/* Human-readable description of the last SGD_EINVAL / launch failure (thread-local). */
+const char *sgd_last_error(void);
+
+/* Library version string. */
+const char *sgd_version(void);
+
+/*
+ * Count/scan stage.  Replaces kernels/plan.py:7-27 (count_scan), launched at
+ * planning/builder.py:8-10.  For r < bcap: chunk[r] = ceil(ceil(L/S)/32)*32,
+ * counts[r] = ceil(L/chunk) (0 for inactive/invalid rows or on error), offsets =
+ * exclusive scan with offsets[bcap] = *record_count; *error = 1 when active is
+ * outside [0, bcap] or an active row has L < 0, L > max_context, S < 1 or S > smax.
+ */
+int sgd_count_scan(const int32_t *lengths, const int32_t *splits, const int32_t *active,
+                   int32_t *counts, int32_t *offsets, int32_t *chunk, int32_t *record_count,
+                   int32_t *error, int32_t bcap, int32_t smax, int32_t max_context, void *stream);
+
+/*
+ * Record emission.  Replaces kernels/plan.py:30-45 (emit_records), launched at
+ * planning/builder.py:15-18.  Writes SoA records (request, split, begin, end,
+ * weight = ceil((end-begin)/block_kv)) at offsets[r] + s for s < counts[r].
+ */
+int sgd_emit_records(const int32_t *lengths, const int32_t *counts, const int32_t *offsets,
+                     const int32_t *chunk, int32_t *request, int32_t *split, int32_t *begin,
+                     int32_t *end, int32_t *weight, int32_t bcap, int32_t smax,
+                     int32_t block_kv, void *stream);
+
+/*
+ * Mode selection, bucket order and packs.  Replaces kernels/plan.py:48-100
+ * (make_order_and_packs), launched at planning/builder.py:19-23.  rules is
+ * [max(rule_count,1)][5] {min_tasks, max_tasks, min_ratio, max_ratio, mode};
+ * last matching rule wins; uniform weights select R1; force_mode >= 0 overrides.
+ */
+int sgd_order_and_packs(const int32_t *weight, const int32_t *record_count, int32_t *order,
+                        int32_t *pack_first, int32_t *pack_count, int32_t *num_packs,
+                        int32_t *mode, const int32_t *rules, int32_t rule_count,
+                        int32_t force_mode, int32_t kv_heads, int32_t workers, int32_t buckets,
+                        int32_t record_capacity, void *stream);
+
+/*
+ * Device LPT lists for STATIC mode.  Replaces kernels/plan.py:103-135
+ * (greedy_lists), launched at planning/builder.py:24-28.  Does nothing unless
+ * *mode == 2.  Produces the lists of planning/reference.py:57-67 (tasks by
+ * (-weight, task), each to the (load, worker)-least worker) as static_head /
+ * static_next (-1 terminated).
+ */
+int sgd_greedy_lists(const int32_t *weight, const int32_t *record_count, const int32_t *mode,
+                     int32_t *static_head, int32_t *static_next, int32_t kv_heads,
+                     int32_t workers, int32_t record_capacity, void *stream);
+
+/* Device plan buffers (all int32, sizes as in runtime/workspace.py:7-23). */
+typedef struct sgd_plan_buffers {
+    int32_t *lengths, *splits, *active;               /* [bcap], [bcap], [1] */
+    int32_t *counts, *offsets, *chunk;                /* [bcap], [bcap+1], [bcap] */
+    int32_t *request, *split, *begin, *end, *weight;  /* [E] */
+    int32_t *order;                                   /* [E] */
+    int32_t *pack_first, *pack_count;                 /* [T] */
+    int32_t *record_count, *num_packs, *mode, *error; /* [1] each */
+    int32_t *static_head, *static_next;               /* [workers], [T] */
+    const int32_t *rules;                             /* [max(rule_count,1)][5] */
+    int32_t rule_count;
+    int32_t batch_capacity, max_splits, max_context, kv_heads, workers, block_kv, buckets;
+} sgd_plan_buffers;
+
+/*
+ * Whole plan build in one launch (count/scan, records, order and packs, and,
+ * when run_greedy != 0, the STATIC lists).  Same results as the four stage
+ * entries above in the order of planning/builder.py:6-28, including the forced
+ * R0 early exit (builder.py:11-14: mode = 0, num_packs = 0, no records).
+ * zero_counters/num_counters: optional int32 array cleared by the same launch
+ * (per-layer claim counters), may be NULL.
+ */
+int sgd_build_plan(const sgd_plan_buffers *plan, int32_t force_mode, int32_t run_greedy,
+                   int32_t *zero_counters, int32_t num_counters, void *stream);
+
+/* Arguments of one persistent decode-attention launch. */
+typedef struct sgd_decode_args {
+    const void *q, *k, *v;          /* q [bcap,Hq,D]; k/v paged [P,page,Hkv,D] or CSR [tok,Hkv,D] */
+    const int32_t *pages;           /* paged: table [bcap, max_pages]; CSR: kv_indices */
+    const int32_t *indptr;          /* CSR: kv_indptr [bcap+1]; NULL when paged */
+    const int32_t *lengths, *request, *split, *begin, *end, *order, *offsets, *chunk;
+    const int32_t *active, *record_count, *mode, *pack_first, *pack_count, *num_packs;
+    int32_t *counter;               /* per-layer claim counter, zero before the launch */
+    const int32_t *static_head, *static_next;
+    float *partial;                 /* [bcap, Hq, smax, D] */
+    float *lse;                     /* [bcap, Hq, smax] */
+    float scale;
+    int32_t _pad0;
+    int64_t q_stride[3], k_stride[4], v_stride[4], pt_stride[2];
+    int32_t query_heads, kv_heads, head_dim, max_splits, page_size, csr, dtype, workers;
+    int32_t kernel;                 /* enum sgd_kernel */
+    int32_t _pad1;
+} sgd_decode_args;
+
+/*
+ * Persistent paged GQA decode attention.  Replaces kernels/attention.py:87-130
+ * (persistent_decode with _attention_task, :12-84), launched at
+ * runtime/engine.py:63-70.  One persistent worker per `workers`; tasks are
+ * (record, kv head); dispatch follows *mode (R0 binary search, R1 stride,
+ * STATIC lists, D1/D4 atomic pack claims on *counter).  Writes the normalized
+ * partial output and natural-log LSE of every task into its (request, q head,
+ * split) slot.
+ */
+int sgd_persistent_decode(const sgd_decode_args *args, void *stream);
+
+/*
+ * Split merge.  Replaces kernels/merge.py:7-30 (merge_splits), launched at
+ * runtime/engine.py:71-73.  For every (r < bcap, h): LSE-weighted merge of the
+ * counts[r] partials in split order; rows with counts[r] == 0 get 0; *error != 0
+ * writes NaN everywhere.  out is [bcap, Hq, D] in `dtype`, contiguous.
+ */
+int sgd_merge_splits(const float *partial, const float *lse, const int32_t *counts,
+                     const int32_t *active, const int32_t *error, void *out, int32_t bcap,
+                     int32_t query_heads, int32_t head_dim, int32_t max_splits, int32_t dtype,
+                     void *stream);
+
+/*
+ * Host (C++) LPT planner: heap assignment of planning/reference.py:57-67 over
+ * host records, written as static lists the way benchmarks/bench_decode.py:14-30
+ * uploads them.  All pointers are HOST pointers: weight[record_count],
+ * static_head[workers], static_next[task_capacity] (every entry written, -1
+ * terminated / unused).
+ */
+int sgd_host_static_lists(const int32_t *weight, int32_t record_count, int32_t kv_heads,
+                          int32_t workers, int32_t task_capacity, int32_t *static_head,
+                          int32_t *static_next);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SGLANG_DECODE_HIP_H */

@@ -1,0 +1,150 @@
+"""Decode-attention parity on the GPU against the FP32 oracle (2e-2 abs / 1e-2 rel),
+for every schedule, both KV layouts (paged, CSR), strides, dtypes and group sizes,
+plus the per-split partial/LSE slots and the invalid-metadata path."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from sglang_decode import workloads as W
+from sglang_decode.config import DecodeConfig, Mode
+from sglang_decode.planning.reference import split_records
+from sglang_decode.runtime.engine import DecodeEngine
+
+from gpu_util import close
+
+pytestmark = pytest.mark.gpu
+
+_CACHE = {}
+
+
+def paged_inputs(c, lengths, seed=17, dtype=torch.bfloat16):
+    key = ("paged", c, tuple(lengths), seed, dtype)
+    if key not in _CACHE:
+        _CACHE.clear()
+        _CACHE[key] = W.make_inputs(c, lengths, seed=seed, dtype=dtype)
+    return _CACHE[key]
+
+
+def run(engine, lengths, inputs, indptr=None, splits=None, scale=None):
+    W.update_plan(engine, lengths, splits)
+    for layer in engine.layers:
+        layer.partial.fill_(float("nan"))
+        layer.lse.fill_(float("nan"))
+    engine.prepare()
+    q, k, v, pages = inputs
+    out = engine.execute(q, k, v, pages, indptr=indptr, scale=scale)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("kernel", ["auto", "generic"])
+@pytest.mark.parametrize("mode", list(Mode))
+@pytest.mark.parametrize("lengths", [[0, 1, 17, 33, 257, 513], [256] * 24 + [1536] * 4 + [16384] * 4])
+def test_outputs_and_plan_every_mode(mode, lengths, kernel):
+    c = DecodeConfig()  # reference defaults: page 16, Bcap 64, Hq/Hkv 32/8, D 128, 108 workers
+    engine = DecodeEngine(c, force_mode=mode, kernel=kernel)
+    inputs = paged_inputs(c, lengths)
+    out = run(engine, lengths, inputs)
+    expected = OA.paged_attention(*inputs[:3], inputs[3], lengths, c.page_size)
+    n = len(lengths)
+    close(out[:n], expected[:n])
+    assert not out[n:].float().abs().sum().item()  # inactive rows are exact zeros
+    assert engine.plan.error.item() == 0
+    records, counts, _ = split_records(lengths, W.split_hints(lengths), c)
+    assert engine.plan.record_count.item() == len(records)
+    assert engine.plan.counts[:n].tolist() == counts
+
+
+def test_partial_and_lse_slots_match_oracle():
+    c = DecodeConfig(batch_capacity=8, max_context=2048, workers=64)
+    lengths = [700, 5, 129, 2048, 1, 300]
+    splits = [3, 1, 2, 16, 1, 4]
+    inputs = paged_inputs(c, lengths, seed=3)
+    engine = DecodeEngine(c, force_mode=Mode.D4)
+    run(engine, lengths, inputs, splits=splits)
+    records, _, _ = split_records(lengths, splits, c)
+    ref = OA.split_partials(*inputs[:3], inputs[3], lengths, c.page_size,
+                            [(r.request, r.split, r.begin, r.end) for r in records],
+                            c.query_heads, c.max_splits)
+    partial = engine.layers[0].partial.cpu().numpy()
+    lse = engine.layers[0].lse.cpu().numpy()
+    got_p = np.stack([partial[r, h, s] for (r, h, s) in ref])
+    got_l = np.array([lse[r, h, s] for (r, h, s) in ref])
+    close(got_p, np.stack([v[0] for v in ref.values()]))
+    close(got_l, np.array([v[1] for v in ref.values()]), atol=1e-2, rtol=1e-3)
+
+
+@pytest.mark.parametrize("mode", [Mode.R1, Mode.STATIC, Mode.D1])
+def test_csr_small_config(mode):
+    c = W.config_for("c1")
+    lengths = W.c1_lengths()
+    q, k, v, indptr, indices = W.make_csr_inputs(c, lengths, seed=5, pool_tokens=4096)
+    engine = DecodeEngine(c, force_mode=mode)
+    out = run(engine, lengths, (q, k, v, indices), indptr=indptr)
+    close(out[:len(lengths)], OA.csr_attention(q, k, v, indptr, indices, lengths)[:len(lengths)])
+
+
+@pytest.mark.parametrize("mode", [Mode.R1, Mode.STATIC, Mode.D1, Mode.D4, Mode.R0])
+def test_csr_llama8b_shape(mode):
+    c = W.config_for("c2")
+    lengths = W.c2_lengths()[:16]
+    q, k, v, indptr, indices = W.make_csr_inputs(c, lengths, seed=9, pool_tokens=1 << 16)
+    engine = DecodeEngine(c, force_mode=mode)
+    out = run(engine, lengths, (q, k, v, indices), indptr=indptr)
+    close(out[:16], OA.csr_attention(q, k, v, indptr, indices, lengths)[:16])
+
+
+def test_noncontiguous_kv_strides():
+    c = DecodeConfig()
+    lengths = [17, 513]
+    q, k, v, pages = W.make_inputs(c, lengths)
+
+    def strided(x):
+        storage = torch.empty((*x.shape[:-1], x.shape[-1] * 2), device=x.device, dtype=x.dtype)
+        storage[..., ::2].copy_(x)
+        return storage[..., ::2]
+
+    ks, vs = strided(k), strided(v)
+    engine = DecodeEngine(c, force_mode=Mode.D4)
+    out = run(engine, lengths, (q, ks, vs, pages))
+    close(out[:2], OA.paged_attention(q, k, v, pages, lengths, c.page_size)[:2])
+    # a transposed (non-contiguous) page table
+    table = pages.t().contiguous().t()
+    out = run(engine, lengths, (q, k, v, table))
+    close(out[:2], OA.paged_attention(q, k, v, pages, lengths, c.page_size)[:2])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hq,hkv,d", [(8, 8, 128), (16, 8, 128), (64, 8, 128), (32, 2, 128),
+                                      (16, 4, 64), (16, 4, 256)])
+def test_group_sizes_dims_dtypes(hq, hkv, d, dtype):
+    c = DecodeConfig(batch_capacity=6, max_context=4096, query_heads=hq, kv_heads=hkv, head_dim=d,
+                     page_size=16, workers=96)
+    lengths = [4096, 1, 999, 64, 0, 2500]
+    inputs = W.make_inputs(c, lengths, seed=11, dtype=dtype)
+    engine = DecodeEngine(c, dtype=dtype, force_mode=Mode.D1)
+    out = run(engine, lengths, inputs, scale=0.07)
+    close(out[:6], OA.paged_attention(*inputs[:3], inputs[3], lengths, c.page_size, scale=0.07))
+
+
+def test_invalid_metadata_writes_nan_and_schedules_nothing():
+    c = DecodeConfig(batch_capacity=4, max_context=512, workers=32)
+    lengths = [100, 600]  # 600 > max_context
+    inputs = W.make_inputs(c, [100, 512])
+    engine = DecodeEngine(c)
+    out = run(engine, lengths, inputs, splits=[1, 1])
+    assert engine.plan.error.item() == 1 and engine.plan.record_count.item() == 0
+    assert torch.isnan(out.float()).all()
+
+
+def test_reused_output_buffer_and_repeated_execute():
+    c = W.config_for("c1")
+    lengths = [200, 16, 100, 50]
+    q, k, v, indptr, indices = W.make_csr_inputs(c, lengths, seed=21)
+    engine = DecodeEngine(c, force_mode=Mode.D4)
+    out1 = run(engine, lengths, (q, k, v, indices), indptr=indptr).clone()
+    out2 = engine.execute(q, k, v, indices, indptr=indptr)  # same plan, second execute
+    torch.cuda.synchronize()
+    assert out2.data_ptr() == engine.layers[0].output.data_ptr()
+    assert torch.equal(out1, out2)

@@ -1,0 +1,96 @@
+"""hipGraph lifecycle: plan rebuilt on every replay, per-layer counters/scratch,
+stable pointers, shrink/regrow, device mode switching, capacity errors."""
+import pytest
+import torch
+
+from oracle import attention as OA
+from sglang_decode import workloads as W
+from sglang_decode.config import DecodeConfig, Mode
+from sglang_decode.planning.policy import PolicyRule
+from sglang_decode.runtime.engine import DecodeEngine, PlanKey
+from sglang_decode.runtime.graph import DecodeGraph
+
+from gpu_util import close
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graph_shrink_regrow_switch_modes_and_reset_layers():
+    c = DecodeConfig(batch_capacity=32, max_context=1024)
+    rules = [PolicyRule(1, c.task_capacity, 101, 10000, int(Mode.D4))]
+    engine = DecodeEngine(c, layers=2, rules=rules)
+    fixtures = [W.make_inputs(c, [1024] * 32, seed=40 + i) for i in range(2)]
+    key = PlanKey("shared-sequence-order", "test-splits", (32, 8, 128))
+    graph = DecodeGraph(engine, [key] * 2, [(x[1], x[2]) for x in fixtures])
+    pointers = [(x.counter.data_ptr(), x.partial.data_ptr(), x.output.data_ptr()) for x in engine.layers]
+    for step, batch in enumerate([32, 7, 1, 32]):
+        lengths = [1024 if i % 3 == 0 else 33 for i in range(batch)]
+        splits = [1] * batch
+        graph.update([x[0][:batch] for x in fixtures], [x[3][:batch] for x in fixtures], lengths, splits)
+        if step == 0:
+            graph.capture()
+        for layer in engine.layers:  # poison everything: every valid result must be rewritten
+            layer.partial.fill_(float("nan"))
+            layer.lse.fill_(float("nan"))
+            layer.counter.fill_(100000)
+        outputs = graph.replay()
+        torch.cuda.synchronize()
+        for layer, x in enumerate(fixtures):
+            expected = OA.paged_attention(*x[:3], x[3], lengths, c.page_size)
+            close(outputs[layer][:batch], expected[:batch])
+        assert pointers == [(x.counter.data_ptr(), x.partial.data_ptr(), x.output.data_ptr())
+                            for x in engine.layers]
+        assert engine.plan.mode.item() == (Mode.R1 if batch == 1 else Mode.D4)
+
+
+def test_capacity_and_layer_compatibility_before_capture():
+    c = DecodeConfig(batch_capacity=2, max_context=1024)
+    engine = DecodeEngine(c, layers=2)
+    x = W.make_inputs(c, [17, 33])
+    first = PlanKey("a", "s", (32, 8, 128))
+    second = PlanKey("b", "s", (32, 8, 128))
+    with pytest.raises(ValueError):
+        DecodeGraph(engine, [first, second], [(x[1], x[2])] * 2)
+    graph = DecodeGraph(engine, [first] * 2, [(x[1], x[2])] * 2)
+    with pytest.raises(ValueError):
+        graph.update([], [], [1, 1, 1], [1, 1, 1])
+    with pytest.raises(ValueError):
+        graph.update([x[0][:2]] * 2, [x[3][:2]] * 2, [17, 2000], [1, 1])
+
+
+@pytest.mark.parametrize("mode", [Mode.R1, Mode.D1, Mode.STATIC])
+def test_csr_graph_replay_shrinking_batches(mode):
+    """Four layers over distinct pools; batch 64 -> 48 -> 17 -> 1 with contexts growing by one."""
+    c = DecodeConfig(batch_capacity=64, max_splits=16, max_context=4096, workers=256)
+    base = W.lognormal_lengths(64, 512, 32, 2048, seed=9)
+    layers = 4
+    pool = sum(base) + 64 * 8
+    fx = [W.make_csr_inputs(c, [x + 3 for x in base], seed=70 + i, pool_tokens=pool)
+          for i in range(layers)]
+    engine = DecodeEngine(c, layers=layers, force_mode=mode)
+    key = PlanKey("batch", "hints", (32, 8, 128))
+    graph = DecodeGraph(engine, [key] * layers, [(x[1], x[2]) for x in fx],
+                        indptrs=[x[4].numel() for x in fx])
+    for step, batch in enumerate([64, 48, 17, 1]):
+        lengths = [x + step for x in base[:batch]]
+        # each layer's kv_indices for this step: the first L tokens of each request's slots
+        indptrs, indices = [], []
+        for x in fx:
+            full_ptr = x[3].cpu().tolist()
+            idx = x[4].cpu()
+            parts = [idx[full_ptr[r]:full_ptr[r] + lengths[r]] for r in range(batch)]
+            ptr = torch.zeros(batch + 1, dtype=torch.int32)
+            ptr[1:] = torch.cumsum(torch.tensor(lengths), 0)
+            indptrs.append(ptr.cuda())
+            indices.append(torch.cat(parts).cuda())
+        graph.update([x[0][:batch] for x in fx], indices, lengths, W.split_hints(lengths, 16), indptrs)
+        if step == 0:
+            graph.capture()
+        for layer in engine.layers:
+            layer.partial.fill_(float("nan"))
+            layer.counter.fill_(7777)
+        outs = graph.replay()
+        torch.cuda.synchronize()
+        for i, x in enumerate(fx):
+            exp = OA.csr_attention(x[0], x[1], x[2], indptrs[i], indices[i], lengths)
+            close(outs[i][:batch], exp[:batch])

@@ -1,0 +1,123 @@
+"""Device plan parity: every stage of the GPU plan is bit-exact against the oracle
+(which tests/test_oracle.py pins to the reference's own planning results)."""
+import pytest
+import torch
+
+from oracle import plan as OP
+from sglang_decode import workloads as W
+from sglang_decode.config import DecodeConfig, Mode
+from sglang_decode.planning.builder import build_plan
+from sglang_decode.planning.policy import PolicyRule
+from sglang_decode.runtime.workspace import PlanBuffers
+
+from gpu_util import assert_plan_equal, cfg_ns, read_plan
+
+pytestmark = pytest.mark.gpu
+
+FORCES = [-1, 0, 1, 2, 3, 4]
+
+
+def load(plan, lengths, splits, active=None):
+    c = plan.config
+    n = len(lengths)
+    lw = torch.zeros(c.batch_capacity, dtype=torch.int32)
+    sw = torch.ones(c.batch_capacity, dtype=torch.int32)
+    lw[:n] = torch.tensor(lengths, dtype=torch.int32)
+    sw[:n] = torch.tensor(splits, dtype=torch.int32)
+    plan.lengths.copy_(lw)
+    plan.splits.copy_(sw)
+    plan.active.fill_(n if active is None else active)
+
+
+def poison(plan):
+    for name in ("counts", "offsets", "chunk", "request", "split", "begin", "end", "weight", "order",
+                 "pack_first", "pack_count", "static_head", "static_next", "record_count",
+                 "num_packs", "mode", "error"):
+        getattr(plan, name).fill_(-7)
+
+
+def run_case(c, lengths, splits, force, fused, rules=(), active=None, name=""):
+    plan = PlanBuffers(c, "cuda", rules)
+    load(plan, lengths, splits, active)
+    poison(plan)
+    build_plan(plan, force, fused=fused)
+    dev = read_plan(plan)
+    act = len(lengths) if active is None else active
+    lw = list(lengths) + [0] * (c.batch_capacity - len(lengths))
+    sw = list(splits) + [1] * (c.batch_capacity - len(splits))
+    flat_rules = [[r.min_tasks, r.max_tasks, r.min_ratio, r.max_ratio, r.mode] for r in rules]
+    ref = OP.full_plan(lw, sw, act, cfg_ns(c), flat_rules, force)
+    if force == 0:
+        ref = dict(ref)  # records are not emitted under forced R0
+    assert_plan_equal(dev, ref, c, act, f"{name} force={force} fused={fused}")
+    return dev
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_plan_matches_oracle_on_benchmark_configs(fused):
+    for name in ("c1", "c2", "c3", "c4", "c5"):
+        c = W.config_for(name)
+        lengths = W.lengths_for(name)
+        splits = W.splits_for(name, lengths, c)
+        for force in FORCES:
+            run_case(c, lengths, splits, force, fused, name=name)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_plan_matches_reference_golden_cases(plan_vectors, fused):
+    for case in plan_vectors:
+        cc = case["config"]
+        c = DecodeConfig(batch_capacity=cc["batch_capacity"], max_splits=cc["max_splits"],
+                         max_context=cc["max_context"], workers=cc["workers"],
+                         kv_heads=cc["kv_heads"], query_heads=cc["kv_heads"] * 4)
+        for force in (3, 4):
+            dev = run_case(c, case["lengths"], case["splits"], force, fused, name=case["name"])
+            n = len(case["records"])
+            assert [[dev[k][i] for k in ("request", "split", "begin", "end", "weight")]
+                    for i in range(n)] == case["records"]
+            assert dev["order"][:n] == case["order"]
+            packs = case["packs_d4" if force == 4 else "packs_d1"]
+            assert [list(p) for p in zip(dev["pack_first"][:dev["num_packs"]],
+                                         dev["pack_count"][:dev["num_packs"]])] == packs
+        dev = run_case(c, case["lengths"], case["splits"], 2, fused, name=case["name"])
+        assert OP.walk_lists(dev["static_head"], dev["static_next"]) == case["static_lists"]
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_plan_error_paths(fused):
+    c = DecodeConfig(batch_capacity=8, max_context=1024, workers=16)
+    for lengths, splits, active in (([10, 2000], [1, 1], None), ([10, 20], [1, 17], None),
+                                    ([10, 20], [0, 1], None), ([-3, 5], [1, 1], None),
+                                    ([10, 20], [1, 1], 9), ([10, 20], [1, 1], -1)):
+        dev = run_case(c, lengths, splits, -1, fused, active=active)
+        assert dev["error"] == 1 and dev["record_count"] == 0
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_plan_rules_and_bypass(fused):
+    c = DecodeConfig(batch_capacity=32, max_context=1024, workers=108)
+    rules = [PolicyRule(1, c.task_capacity, 101, 10000, int(Mode.D4))]
+    for batch in (32, 7, 1):
+        lengths = [1024 if i % 3 == 0 else 33 for i in range(batch)]
+        dev = run_case(c, lengths, [1] * batch, -1, fused, rules=rules)
+        assert dev["mode"] == (Mode.R1 if batch == 1 else Mode.D4)
+    static_rule = [PolicyRule(0, 10 ** 6, 100, 10000, int(Mode.STATIC))]
+    dev = run_case(c, [1024, 33, 33], [1, 1, 1], -1, fused, rules=static_rule)
+    assert dev["mode"] == Mode.STATIC
+
+
+def test_plan_zero_batch_and_edges():
+    c = DecodeConfig(batch_capacity=64, max_context=32768, workers=256)
+    for lengths in ([], [0], [0, 0, 0], [1], [32768], [31, 32, 33, 63, 64, 65]):
+        splits = W.split_hints(lengths, 16) if lengths else []
+        for force in FORCES:
+            run_case(c, lengths, splits, force, True)
+
+
+def test_fused_plan_clears_counters():
+    c = W.config_for("c1")
+    plan = PlanBuffers(c, "cuda")
+    load(plan, [17, 200], [1, 2])
+    counters = torch.full((5,), 1234, dtype=torch.int32, device="cuda")
+    build_plan(plan, -1, counters=counters)
+    assert counters.tolist() == [0] * 5

@@ -1,0 +1,200 @@
+"""Host-side tests (no GPU): config and policy contracts, the host planning API
+against the reference's golden sequences, the C++ host LPT planner, the C-ABI
+library's exports, and the engine's host validation (ValueError before any launch)."""
+import ctypes
+import json
+import os
+import re
+import types
+
+import pytest
+
+from sglang_decode.config import DecodeConfig, Mode
+from sglang_decode.planning import reference as R
+from sglang_decode.planning.policy import PolicyRule, load_policy
+from sglang_decode import workloads as W
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+# ------------------------------------------------------------------ config / policy
+
+def test_config_defaults_and_derived():
+    c = DecodeConfig()
+    assert (c.batch_capacity, c.max_splits, c.max_context, c.query_heads, c.kv_heads, c.head_dim,
+            c.page_size, c.workers, c.block_kv, c.split_alignment) == (64, 16, 32768, 32, 8, 128, 16,
+                                                                       108, 128, 32)
+    assert c.group_size == 4 and c.record_capacity == 1024 and c.task_capacity == 8192
+    assert c.max_pages == 2048 and c.buckets == 9
+    assert W.config_for("c1").buckets == 2 and W.config_for("c2").buckets == 7
+    assert W.config_for("c4").buckets == 8 and W.config_for("c4").max_pages == 1024
+
+
+@pytest.mark.parametrize("kw", [dict(batch_capacity=0), dict(query_heads=24, kv_heads=8),
+                                dict(query_heads=64, kv_heads=2), dict(head_dim=96),
+                                dict(block_kv=64), dict(split_alignment=16),
+                                dict(batch_capacity=1024, max_splits=32), dict(workers=5000)])
+def test_config_rejects(kw):
+    with pytest.raises(ValueError):
+        DecodeConfig(**kw)
+
+
+def test_config_lifts_reference_record_bound_for_c3():
+    c = W.config_for("c3")
+    assert c.record_capacity == 8192 and c.task_capacity == 65536
+
+
+def test_policy_gate(tmp_path):
+    assert load_policy() == []
+    path = tmp_path / "p.json"
+    path.write_text(json.dumps({"status": "unvalidated", "evidence": [], "rules": []}))
+    with pytest.raises(ValueError):
+        load_policy(path)
+    path.write_text(json.dumps({"status": "validated", "evidence": [], "rules": []}))
+    with pytest.raises(ValueError):
+        load_policy(path)
+    good = {"status": "validated", "evidence": [{"path": "x", "sha256": "0"}],
+            "rules": [dict(min_tasks=1, max_tasks=100, min_ratio=101, max_ratio=900, mode=4)]}
+    path.write_text(json.dumps(good))
+    assert load_policy(path) == [PolicyRule(1, 100, 101, 900, 4)]
+    for bad in (dict(mode=0), dict(min_ratio=99), dict(max_tasks=0), dict(min_tasks=-1)):
+        row = dict(good["rules"][0], **bad)
+        path.write_text(json.dumps(dict(good, rules=[row])))
+        with pytest.raises(ValueError):
+            load_policy(path)
+
+
+# ------------------------------------------------------------------ host planning API
+
+def _cfg(case):
+    cc = case["config"]
+    return types.SimpleNamespace(**cc)
+
+
+def test_host_planning_matches_reference_sequences(plan_vectors):
+    for case in plan_vectors:
+        c = _cfg(case)
+        records, counts, offsets = R.split_records(case["lengths"], case["splits"], c)
+        assert [[r.request, r.split, r.begin, r.end, r.weight] for r in records] == case["records"]
+        assert counts == case["counts"] and offsets == case["offsets"]
+        order = R.bucket_order(records)
+        assert order == case["order"], case["name"]
+        assert [list(p) for p in R.make_packs(records, order, c.kv_heads, c.workers, 1)] == case["packs_d1"]
+        assert [list(p) for p in R.make_packs(records, order, c.kv_heads, c.workers, 4)] == case["packs_d4"]
+        assert R.greedy_static(records, c.kv_heads, c.workers) == case["static_lists"]
+        R.validate_plan(records, order, R.make_packs(records, order, c.kv_heads, c.workers), c.kv_heads)
+
+
+@pytest.mark.parametrize("lengths,splits", [([32769], [1]), ([1], [0]), ([1] * 65, [1] * 65)])
+def test_host_capacity_rejected(lengths, splits):
+    with pytest.raises(ValueError):
+        R.split_records(lengths, splits, DecodeConfig())
+
+
+def test_validate_plan_catches_duplicates():
+    c = DecodeConfig()
+    records, _, _ = R.split_records([300, 40], [2, 1], c)
+    order = R.bucket_order(records)
+    packs = R.make_packs(records, order, c.kv_heads, c.workers)
+    R.validate_plan(records, order, packs, c.kv_heads)
+    with pytest.raises(AssertionError):
+        R.validate_plan(records, order, packs + [packs[0]], c.kv_heads)
+
+
+def test_split_hints_rule():
+    assert W.split_hints([512] * 24 + [8192] * 8) == [1] * 24 + [16] * 8
+    assert W.split_hints([256] * 24 + [1536] * 4 + [16384] * 4) == [1] * 24 + [2] * 4 + [16] * 4
+    assert W.split_hints([0, 0]) == [1, 1]
+
+
+def test_seeded_workloads_are_deterministic():
+    assert W.c2_lengths() == W.c2_lengths()
+    c2 = W.c2_lengths()
+    assert len(c2) == 64 and min(c2) >= 128 and max(c2) <= 8192
+    c3 = W.c3_lengths()
+    assert c3[:2] == [32768, 32768] and len(c3) == 128 and all(32 <= x <= 512 for x in c3[2:])
+    c4 = W.c4_lengths()
+    assert len(c4) == 32 and all(2048 <= x <= 16384 for x in c4)
+    assert W.algorithmic_bytes([1000, 24], W.config_for("c2")) == (
+        1024 * 8 * 128 * 2 * 2 + 4 * 1024 + 2 * 32 * 128 * 4)
+
+
+# ------------------------------------------------------------------ native library
+
+def _header_symbols():
+    text = open(os.path.join(ROOT, "include", "sglang_decode_hip.h")).read()
+    return sorted(set(re.findall(r"\b(sgd_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from sglang_decode import _lib
+    handle = _lib.lib()
+    symbols = _header_symbols()
+    assert len(symbols) >= 10
+    for name in symbols:
+        assert hasattr(handle, name), name
+    assert b"gfx950" in handle.sgd_version()
+
+
+def test_struct_layouts_match_header():
+    from sglang_decode._lib import DecodeArgsC, PlanBuffersC
+    # 24 pointers, scale + pad, 13 int64 strides, 10 int32 -> 24*8 + 8 + 104 + 40
+    assert ctypes.sizeof(DecodeArgsC) == 24 * 8 + 8 + 13 * 8 + 10 * 4
+    assert DecodeArgsC.q_stride.offset == 24 * 8 + 8
+    assert ctypes.sizeof(PlanBuffersC) == 21 * 8 + 8 * 4
+
+
+def test_host_static_lists_cpp_matches_reference(plan_vectors):
+    from sglang_decode import _lib
+    lib = _lib.lib()
+    for case in plan_vectors:
+        c = _cfg(case)
+        weights = [r[4] for r in case["records"]]
+        n = len(weights)
+        cap = c.batch_capacity * c.max_splits * c.kv_heads
+        w = (ctypes.c_int32 * max(n, 1))(*weights)
+        heads = (ctypes.c_int32 * c.workers)()
+        nxt = (ctypes.c_int32 * cap)()
+        assert lib.sgd_host_static_lists(w, n, c.kv_heads, c.workers, cap, heads, nxt) == 0
+        lists = R.lists_to_links(case["static_lists"], c.workers, cap)
+        assert list(heads) == lists[0] and list(nxt) == lists[1], case["name"]
+
+
+def test_abi_rejects_bad_arguments_before_launch():
+    from sglang_decode import _lib
+    lib = _lib.lib()
+    assert lib.sgd_count_scan(None, None, None, None, None, None, None, None, 0, 16, 256, None) == -22
+    assert b"bcap" in lib.sgd_last_error()
+    args = _lib.DecodeArgsC()
+    args.query_heads, args.kv_heads, args.head_dim = 32, 8, 96
+    assert lib.sgd_persistent_decode(ctypes.byref(args), None) == -22
+    with pytest.raises(ValueError):
+        _lib.check(-22, "x")
+
+
+# ------------------------------------------------------------------ engine host validation
+
+def test_engine_validates_before_launch():
+    import torch
+    from sglang_decode.runtime.engine import DecodeEngine
+    c = W.config_for("c1")
+    engine = DecodeEngine(c, device="cpu", layers=1)
+    q = torch.zeros(c.batch_capacity, c.query_heads, c.head_dim, dtype=torch.bfloat16)
+    k = torch.zeros(10, 1, c.kv_heads, c.head_dim, dtype=torch.bfloat16)
+    pages = torch.zeros(c.batch_capacity, c.max_pages, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        engine.execute(q.float(), k, k, pages)
+    with pytest.raises(ValueError):
+        engine.execute(q[:2], k, k, pages)
+    with pytest.raises(ValueError):
+        engine.execute(q, k[:, :, :1], k[:, :, :1], pages)
+    with pytest.raises(ValueError):
+        engine.execute(q, k, k, pages[:, :3])
+    with pytest.raises(ValueError):  # CSR needs 3-D KV
+        engine.execute(q, k, k, pages.flatten(), indptr=torch.zeros(5, dtype=torch.int32))
+    with pytest.raises(ValueError):  # index dtype
+        engine.execute(q, k, k, pages.long())
+    assert engine.plan.rules.tolist() == [[0, 0, 100, 100, 1]] and engine.plan.rule_count == 0
+    assert engine.layers[0].partial.shape == (4, 8, 16, 128)
+    assert engine.layers[0].lse.shape == (4, 8, 16)
+    assert Mode.D4 == 4
