@@ -61,7 +61,7 @@ def test_capacity_and_layer_compatibility_before_capture():
 @pytest.mark.parametrize("mode", [Mode.R1, Mode.D1, Mode.STATIC])
 def test_csr_graph_replay_shrinking_batches(mode):
     """Four layers over distinct pools; batch 64 -> 48 -> 17 -> 1 with contexts growing by one."""
-    c = DecodeConfig(batch_capacity=64, max_splits=16, max_context=4096, workers=256)
+    c = DecodeConfig(batch_capacity=64, max_splits=16, max_context=4096, page_size=1, workers=256)
     base = W.lognormal_lengths(64, 512, 32, 2048, seed=9)
     layers = 4
     pool = sum(base) + 64 * 8
