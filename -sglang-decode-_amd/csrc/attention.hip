@@ -5,6 +5,8 @@
 
 namespace sgd {
 int launch_attention_generic(const sgd_decode_args &a, bool vec, hipStream_t stream);
+int launch_attention_valu(const sgd_decode_args &a, hipStream_t stream);
+bool valu_supported(const sgd_decode_args &a);
 }
 
 using namespace sgd;
@@ -43,8 +45,15 @@ extern "C" int sgd_persistent_decode(const sgd_decode_args *args, void *stream) 
     clear_stale_error();
     switch (a.kernel) {
         case SGD_KERNEL_AUTO:
+            if (valu_supported(a)) return launch_attention_valu(a, (hipStream_t)stream);
+            return launch_attention_generic(a, vec, (hipStream_t)stream);
         case SGD_KERNEL_GENERIC:
             return launch_attention_generic(a, vec, (hipStream_t)stream);
+        case SGD_KERNEL_VALU:
+            if (!valu_supported(a))
+                return einval("persistent_decode: the VALU kernel needs group <= 4, head_dim 128, unit dim "
+                              "stride, 16-byte aligned rows and a power-of-two page size");
+            return launch_attention_valu(a, (hipStream_t)stream);
         default:
             return einval("persistent_decode: kernel %d not available", a.kernel);
     }
