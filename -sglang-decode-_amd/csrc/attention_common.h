@@ -93,6 +93,18 @@ __device__ void for_each_task(const sgd_decode_args &a, int32_t *sh_cursor, Run 
             cursor += a.workers;
         }
     }
+    // The last worker to finish puts the claim counter back to zero for the next
+    // launch.  Relaxed is enough: a worker reaches this increment only after its
+    // final claim returned (the loop exit depends on that value), so every claim
+    // has been performed before the last increment is observed.  (A device-scope
+    // release here would write back the XCD's whole L2 once per workgroup.)
+    if (a.done_counter && threadIdx.x == 0) {
+        const int32_t done = __hip_atomic_fetch_add(a.done_counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == a.workers - 1) {
+            __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.done_counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 }  // namespace sgd

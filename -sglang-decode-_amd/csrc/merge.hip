@@ -1,15 +1,34 @@
 // Split merge: per (request, query head), LSE-weighted combination of the
-// normalized partial outputs of its splits, in split order (kernels/merge.py:7-30).
+// normalized partial outputs of its splits (kernels/merge.py:7-30).
 //
-// One wave per (request, head); each lane owns head_dim/64 consecutive dims, so
-// every partial row is read as one coalesced 256-1024 B burst.  Rows with no
-// split produce exact zeros (acc 0 / max(den, 1e-30)); a plan error produces NaN.
+// One wave per (request, head).  The merge is latency-bound (a few KB per row),
+// so nothing waits on a dependent chain: the split LSEs are loaded one per lane
+// in a single access, the global max and the weights exp(lse_s - max) come from
+// wave reductions, and the partial rows (each a coalesced 256-1024 B burst, lanes
+// owning head_dim/64 consecutive dims) are then streamed with independent loads.
+// This is the two-pass form of the reference's running-max merge (same value up
+// to rounding).  Rows with no split produce exact zeros (0 / max(den, 1e-30)); a
+// plan error produces NaN.
 #include "common.h"
 
 namespace sgd {
 namespace {
 
 constexpr int kMergeWaves = 4;
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int DPL>
+__device__ __forceinline__ void load_row(const float *src, float (&v)[DPL]) {
+    if constexpr (DPL == 4) {
+        const float4 t = *reinterpret_cast<const float4 *>(src);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else if constexpr (DPL == 2) {
+        const float2 t = *reinterpret_cast<const float2 *>(src);
+        v[0] = t.x; v[1] = t.y;
+    } else {
+        v[0] = src[0];
+    }
+}
 
 template <int DT, int DPL>  // DPL = dims per lane
 __global__ __launch_bounds__(64 * kMergeWaves) void k_merge(const float *__restrict__ partial,
@@ -25,29 +44,26 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge(const float *__restr
     if (head >= hq) return;
     const int32_t n = counts[r];
     const int64_t row = (int64_t)r * hq + head;
-    float m = -INFINITY, den = 0.f, acc[DPL];
+    const float *lrow = lse + row * smax;
+    float mx = -INFINITY;
+    for (int b = 0; b < n; b += 64)
+        mx = fmaxf(mx, wave_max(b + lane < n ? lrow[b + lane] * kLog2e : -INFINITY));
+    float den = 0.f, acc[DPL];
 #pragma unroll
     for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
-    for (int s = 0; s < n; ++s) {
-        const int64_t slot = row * smax + s;
-        const float l = lse[slot];
-        const float *src = partial + slot * D + lane * DPL;
-        float v[DPL];
-        if constexpr (DPL == 4) {
-            const float4 t = *reinterpret_cast<const float4 *>(src);
-            v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-        } else if constexpr (DPL == 2) {
-            const float2 t = *reinterpret_cast<const float2 *>(src);
-            v[0] = t.x; v[1] = t.y;
-        } else {
-            v[0] = src[0];
-        }
-        const float nm = fmaxf(m, l);
-        const float ow = __expf(m - nm), w = __expf(l - nm);
+    const float *prow = partial + row * smax * D + lane * DPL;
+    for (int b = 0; b < n; b += 64) {
+        const float w = b + lane < n ? __builtin_amdgcn_exp2f(lrow[b + lane] * kLog2e - mx) : 0.f;
+        den += wave_sum(w);
+        const int cnt = min(64, n - b);
+#pragma unroll 4
+        for (int s = 0; s < cnt; ++s) {
+            const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
+            float v[DPL];
+            load_row<DPL>(prow + (int64_t)(b + s) * D, v);
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) acc[i] = acc[i] * ow + v[i] * w;
-        den = den * ow + w;
-        m = nm;
+            for (int i = 0; i < DPL; ++i) acc[i] += v[i] * ws;
+        }
     }
     const bool bad = *error != 0;
     const float inv = 1.0f / fmaxf(den, 1.0e-30f);

@@ -33,7 +33,7 @@ class DecodeArgsC(ctypes.Structure):
     _fields_ = [(name, _P) for name in (
         "q", "k", "v", "pages", "indptr", "lengths", "request", "split", "begin", "end", "order",
         "offsets", "chunk", "active", "record_count", "mode", "pack_first", "pack_count",
-        "num_packs", "counter", "static_head", "static_next", "partial", "lse")] + [
+        "num_packs", "counter", "done_counter", "static_head", "static_next", "partial", "lse")] + [
         ("scale", ctypes.c_float), ("_pad0", _I),
         ("q_stride", ctypes.c_int64 * 3), ("k_stride", ctypes.c_int64 * 4),
         ("v_stride", ctypes.c_int64 * 4), ("pt_stride", ctypes.c_int64 * 2)] + [

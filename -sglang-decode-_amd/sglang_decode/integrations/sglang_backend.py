@@ -14,14 +14,14 @@ class that provides the upstream attributes (used by the host-side tests).
 Environment: DECODE_DISABLE=1 keeps upstream decode; DECODE_MODE=AUTO|R0|R1|
 STATIC|D1|D4 forces a schedule; DECODE_POLICY=<validated policy json>;
 DECODE_BATCH_CAPACITY (default 64); DECODE_REUSE_PLAN=0 rebuilds the plan on
-every layer; DECODE_WORKERS overrides the persistent worker count (default: the
-device's CU count).
+every layer; DECODE_WORKERS overrides the persistent worker count (default: two
+per compute unit).
 """
 import os
 
 import torch
 
-from ..config import DecodeConfig, Mode
+from ..config import WORKGROUPS_PER_CU, DecodeConfig, Mode
 from ..planning.policy import load_policy
 
 try:  # pragma: no cover - depends on an optional install
@@ -74,7 +74,8 @@ def make_backend_class(base):
             if found is None:
                 return
             dtype, head_dim = found
-            workers = int(os.getenv("DECODE_WORKERS", "0")) or max(1, self.device_core_count)
+            workers = (int(os.getenv("DECODE_WORKERS", "0"))
+                       or WORKGROUPS_PER_CU * max(1, self.device_core_count))
             config = DecodeConfig(
                 batch_capacity=int(os.getenv("DECODE_BATCH_CAPACITY", "64")),
                 max_splits=self.max_kv_splits, max_context=self.max_context_len,

@@ -22,6 +22,8 @@ def persistent_decode(plan, layer, q, k, v, pages, indptr, scale, k_strides, v_s
                  "static_head", "static_next"):
         setattr(a, name, getattr(plan, name).data_ptr())
     a.counter = layer.counter.data_ptr()
+    done = getattr(layer, "done", None)
+    a.done_counter = done.data_ptr() if done is not None else None
     a.partial = layer.partial.data_ptr()
     a.lse = layer.lse.data_ptr()
     a.scale = float(scale)

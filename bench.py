@@ -41,7 +41,7 @@ def parse():
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--policies", default=",".join(POLICIES))
     ap.add_argument("--kernel", default="auto")
-    ap.add_argument("--workers", type=int, default=0, help="0 = CU count")
+    ap.add_argument("--workers", type=int, default=0, help="0 = default_workers (2 per CU)")
     ap.add_argument("--kernel-launches", type=int, default=200,
                     help="attention-only launches timed for the roofline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -61,7 +61,7 @@ def main():
     import torch
 
     from sglang_decode import workloads as W
-    from sglang_decode.config import DecodeConfig, Mode
+    from sglang_decode.config import Mode, default_workers
     from sglang_decode.kernels.attention import persistent_decode
     from sglang_decode.runtime.engine import DecodeEngine, PlanKey
     from sglang_decode.runtime.graph import DecodeGraph
@@ -69,7 +69,7 @@ def main():
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     props = torch.cuda.get_device_properties(dev)
-    workers = args.workers or props.multi_processor_count
+    workers = args.workers or default_workers(dev)
     base = W.config_for("c2", workers=workers)
     c = base
     lengths = W.c2_lengths()

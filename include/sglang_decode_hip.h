@@ -124,6 +124,9 @@ typedef struct sgd_decode_args {
     const int32_t *lengths, *request, *split, *begin, *end, *order, *offsets, *chunk;
     const int32_t *active, *record_count, *mode, *pack_first, *pack_count, *num_packs;
     int32_t *counter;               /* per-layer claim counter, zero before the launch */
+    int32_t *done_counter;          /* optional (may be NULL): workers that finished; the last
+                                       one resets *counter and *done_counter to 0, so the pair is
+                                       zero again for the next launch */
     const int32_t *static_head, *static_next;
     float *partial;                 /* [bcap, Hq, smax, D] */
     float *lse;                     /* [bcap, Hq, smax] */

@@ -138,9 +138,9 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layouts_match_header():
     from sglang_decode._lib import DecodeArgsC, PlanBuffersC
-    # 24 pointers, scale + pad, 13 int64 strides, 10 int32 -> 24*8 + 8 + 104 + 40
-    assert ctypes.sizeof(DecodeArgsC) == 24 * 8 + 8 + 13 * 8 + 10 * 4
-    assert DecodeArgsC.q_stride.offset == 24 * 8 + 8
+    # 25 pointers, scale + pad, 13 int64 strides, 10 int32
+    assert ctypes.sizeof(DecodeArgsC) == 25 * 8 + 8 + 13 * 8 + 10 * 4
+    assert DecodeArgsC.q_stride.offset == 25 * 8 + 8
     assert ctypes.sizeof(PlanBuffersC) == 21 * 8 + 8 * 4
 
 
