@@ -6,7 +6,9 @@
 namespace sgd {
 int launch_attention_generic(const sgd_decode_args &a, bool vec, hipStream_t stream);
 int launch_attention_valu(const sgd_decode_args &a, hipStream_t stream);
+int launch_attention_stream(const sgd_decode_args &a, hipStream_t stream);
 bool valu_supported(const sgd_decode_args &a);
+bool stream_supported(const sgd_decode_args &a);
 }
 
 using namespace sgd;
@@ -22,6 +24,19 @@ bool vector_layout(const sgd_decode_args &a) {
     for (int i = 0; i < 3; ++i)
         if (a.k_stride[i] % 8 != 0 || a.v_stride[i] % 8 != 0) return false;
     return true;
+}
+
+// Compute units of the current device (a host query, cached per device).
+int device_cus() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cache[dev] = n;
+    }
+    return cache[dev];
 }
 
 }  // namespace
@@ -45,6 +60,10 @@ extern "C" int sgd_persistent_decode(const sgd_decode_args *args, void *stream) 
     clear_stale_error();
     switch (a.kernel) {
         case SGD_KERNEL_AUTO:
+            // The stream kernel is one 1024-thread workgroup per CU: with more workers
+            // than CUs they would run in turns, so the two-per-CU kernel takes over.
+            if (stream_supported(a) && a.workers <= device_cus())
+                return launch_attention_stream(a, (hipStream_t)stream);
             if (valu_supported(a)) return launch_attention_valu(a, (hipStream_t)stream);
             return launch_attention_generic(a, vec, (hipStream_t)stream);
         case SGD_KERNEL_GENERIC:
@@ -54,6 +73,11 @@ extern "C" int sgd_persistent_decode(const sgd_decode_args *args, void *stream) 
                 return einval("persistent_decode: the VALU kernel needs group <= 4, head_dim 128, unit dim "
                               "stride, 16-byte aligned rows and a power-of-two page size");
             return launch_attention_valu(a, (hipStream_t)stream);
+        case SGD_KERNEL_STREAM:
+            if (!stream_supported(a))
+                return einval("persistent_decode: the stream kernel needs group <= 4, head_dim 128, unit dim "
+                              "stride, 16-byte aligned rows and partial, and a power-of-two page size");
+            return launch_attention_stream(a, (hipStream_t)stream);
         default:
             return einval("persistent_decode: kernel %d not available", a.kernel);
     }

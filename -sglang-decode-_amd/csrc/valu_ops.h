@@ -1,0 +1,268 @@
+// Wave64 building blocks shared by the VALU decode-attention kernels: packed
+// 16-bit dot products, DPP cross-lane moves, the paged/CSR row gather of one
+// 16-token tile, and the tile's QK^T / online-softmax / P.V math.
+#pragma once
+
+#include "attention_common.h"
+
+namespace sgd {
+namespace valu {
+
+constexpr int kTile = 16;                 // tokens per wave per tile
+constexpr int kD = 128;                   // head_dim
+constexpr int kHeads = 4;                 // padded query-head group
+constexpr int kRowsLoads = kTile / 4;     // 16-byte loads per K (and per V) tile: 4 rows each
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// One wave's staging area: the K and V rows of a 16-token tile (row-major, 256 B
+// rows) and the tile's probabilities as token pairs.
+struct WaveTile {
+    uint4 k[kTile][kD / 8];          // 4 KB
+    uint4 v[kTile][kD / 8];          // 4 KB
+    uint4 p[kTile / 2];              // [pair] -> 4 heads x (p[2i], p[2i+1]) in the KV dtype
+};
+
+template <int DT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    if constexpr (DT == SGD_BF16)
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                               false);
+    else
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    if constexpr (DT == SGD_BF16) {
+        bf16x2 r = {(__bf16)lo, (__bf16)hi};
+        return __builtin_bit_cast(uint32_t, r);
+    } else {
+        f16x2 r = {(_Float16)lo, (_Float16)hi};
+        return __builtin_bit_cast(uint32_t, r);
+    }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf,
+                                                                  false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+    return __builtin_amdgcn_mov_dpp(x, CTRL, 0xf, 0xf, false);
+}
+
+__device__ __forceinline__ int32_t uni(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ float uni_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+}
+__device__ __forceinline__ float lane_f(float x, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+
+constexpr int kQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kQuadXor3 = 0x1B;       // quad_perm [3,2,1,0]
+constexpr int kRowShl8 = 0x108;       // row_shl:8
+constexpr int kRowRor8 = 0x128;       // row_ror:8
+constexpr int kRowHalfMirror = 0x141; // row_half_mirror
+constexpr int kRowNewBcast = 0x150;   // row_newbcast:n
+
+// The lane that holds head h after the QK reduce-scatter (lanes 0, 2, 4, 6).
+__device__ __forceinline__ constexpr int head_lane(int h) { return ((h >> 1) << 2) | ((h & 1) << 1); }
+
+// Lane roles.  QK: 8 lanes per token; qg = lane / 8 picks the token, qj = lane % 8
+// owns the 16 B chunks qj and qj + 8; after the reduce-scatter the lane holds head
+// hs = 2*bit2(qj) + bit1(qj).  P.V: half ph = lane / 32 takes token pairs 2s + ph;
+// pd = lane % 32 owns dims 4*pd .. 4*pd+3.
+struct Roles {
+    int qg, qj, hs, ph, pd;
+    bool b2, b1;
+    __device__ __forceinline__ explicit Roles(int l) {
+        qg = l >> 3;
+        qj = l & 7;
+        hs = ((qj >> 2) << 1) | ((qj >> 1) & 1);
+        b2 = (qj & 4) != 0;
+        b1 = (qj & 2) != 0;
+        ph = l >> 5;
+        pd = l & 31;
+    }
+};
+
+// Where a tile's rows come from.
+struct TileSrc {
+    const char *kbase, *vbase;  // K/V + group * head stride (bytes)
+    int64_t kp, kt, vp, vt;     // page and in-page strides (bytes)
+    int32_t request, ind0, start, end;
+};
+
+// lane 16r + i (i < kRowsLoads) fetches the page/slot index of token tok0 + 4i + r
+template <bool CSR>
+__device__ __forceinline__ int32_t tile_index(const sgd_decode_args &a, const TileSrc &t, int32_t tok0, int lane,
+                                              int page_shift) {
+    const int r = lane >> 4, i = lane & 15;
+    const int32_t tok = tok0 + 4 * i + r;
+    int32_t v = 0;
+    if (i < kRowsLoads && tok < t.end) {
+        if constexpr (CSR) v = a.pages[t.ind0 + tok];
+        else v = a.pages[(int64_t)t.request * a.pt_stride[0] + (int64_t)(tok >> page_shift) * a.pt_stride[1]];
+    }
+    return v;
+}
+
+// 4 x 16-byte loads for K and for V, each covering 4 token rows of 256 B (16 lanes
+// per row); DPP row_newbcast hands each row its token's index.  The loads are
+// unconditional, so no exec-mask branch sits between a tile's loads and the
+// compute they overlap: rows past `end` got index 0 from tile_index, which
+// addresses a row of page 0 (in bounds), and tile_stage zeroes them.
+template <bool CSR>
+__device__ __forceinline__ void tile_issue(const TileSrc &t, int32_t tile, int32_t idxv, int32_t page_mask, int lane,
+                                           uint4 (&kr)[kRowsLoads], uint4 (&vr)[kRowsLoads]) {
+    const int r = lane >> 4, c = lane & 15;
+    const int32_t tok0 = t.start + tile * kTile;
+#define SGD_LOAD_ROW(I)                                                                              \
+    {                                                                                                \
+        const uint32_t phys = (uint32_t)dpp_i<kRowNewBcast + I>(idxv);                               \
+        int64_t ko = (int64_t)phys * t.kp + c * 16, vo = (int64_t)phys * t.vp + c * 16;              \
+        if constexpr (!CSR) {                                                                        \
+            const int32_t inner = (tok0 + 4 * I + r) & page_mask;                                    \
+            ko += (int64_t)inner * t.kt;                                                             \
+            vo += (int64_t)inner * t.vt;                                                             \
+        }                                                                                            \
+        kr[I] = *reinterpret_cast<const uint4 *>(t.kbase + ko);                                      \
+        vr[I] = *reinterpret_cast<const uint4 *>(t.vbase + vo);                                      \
+    }
+    static_assert(kRowsLoads == 4, "one SGD_LOAD_ROW per 4-row load");
+    SGD_LOAD_ROW(0) SGD_LOAD_ROW(1) SGD_LOAD_ROW(2) SGD_LOAD_ROW(3)
+#undef SGD_LOAD_ROW
+}
+
+// Writes the tile's rows to the wave's LDS tile.  In a partial tile (nvalid < 16,
+// uniform) the rows past the task's end are zero: their probabilities are exactly
+// zero, and zero V keeps P.V finite whatever page 0 holds.
+__device__ __forceinline__ void tile_stage(WaveTile &wt, uint4 (&kr)[kRowsLoads], uint4 (&vr)[kRowsLoads], int lane,
+                                           int32_t nvalid) {
+    if (nvalid < kTile) {
+#pragma unroll
+        for (int i = 0; i < kRowsLoads; ++i)
+            if (4 * i + (lane >> 4) >= nvalid) {
+                kr[i] = make_uint4(0, 0, 0, 0);
+                vr[i] = make_uint4(0, 0, 0, 0);
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < kRowsLoads; ++i) {
+        wt.k[4 * i + (lane >> 4)][lane & 15] = kr[i];
+        wt.v[4 * i + (lane >> 4)][lane & 15] = vr[i];
+    }
+}
+
+// One staged tile: QK^T against the group's q rows `qs` (LDS), online softmax in
+// the exp2 domain, P.V into acc.  m_l/den_l are this lane's head's running max and
+// denominator (QK roles); acc holds 4 heads x 4 dims (P.V roles).
+template <int DT>
+__device__ __forceinline__ void tile_compute(WaveTile &wt, const uint4 (*qs)[kD / 8], int32_t nvalid, float scale2,
+                                             const Roles &ro, float &m_l, float &den_l, float (&acc)[kHeads][4]) {
+    constexpr int kPasses = kTile / 8;
+    float s[kPasses];
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+        const int tk = 8 * pass + ro.qg;
+        const uint4 lo = wt.k[tk][ro.qj], hi = wt.k[tk][ro.qj + 8];
+        const uint32_t kv[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        float sh4[kHeads];
+#pragma unroll
+        for (int h = 0; h < kHeads; ++h) {
+            const uint4 ql = qs[h][ro.qj], qh = qs[h][ro.qj + 8];
+            const uint32_t qv[8] = {ql.x, ql.y, ql.z, ql.w, qh.x, qh.y, qh.z, qh.w};
+            float x = 0.f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) x = dot2<DT>(qv[q], kv[q], x);
+            sh4[h] = x;
+        }
+        // reduce-scatter over the 8 lanes of the token
+        float k0 = ro.b2 ? sh4[2] : sh4[0], k1 = ro.b2 ? sh4[3] : sh4[1];
+        const float s0 = ro.b2 ? sh4[0] : sh4[2], s1 = ro.b2 ? sh4[1] : sh4[3];
+        k0 += dpp<kRowHalfMirror>(s0);
+        k1 += dpp<kRowHalfMirror>(s1);
+        float kk = ro.b1 ? k1 : k0;
+        const float ss = ro.b1 ? k0 : k1;
+        kk += dpp<kQuadXor3>(ss);
+        kk += dpp<kQuadXor1>(kk);
+        s[pass] = (tk < nvalid) ? kk * scale2 : -INFINITY;
+    }
+    // max over the tile for head hs
+    float mx = fmaxf(s[0], s[1]);
+    mx = fmaxf(mx, dpp<kRowRor8>(mx));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_l, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m_l - m_new);
+    m_l = m_new;
+    float p[kPasses];
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) p[pass] = __builtin_amdgcn_exp2f(s[pass] - m_new);
+    den_l = den_l * alpha + (p[0] + p[1]);
+    // pairs (8*pass + qg, +1) for even qg, written once per (pair, head)
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+        const float pn = dpp<kRowShl8>(p[pass]);
+        if (((ro.qg & 1) == 0) && ((ro.qj & 1) == 0)) {
+            uint32_t *prow = reinterpret_cast<uint32_t *>(&wt.p[4 * pass + (ro.qg >> 1)]);
+            prow[ro.hs] = pack2<DT>(p[pass], pn);
+        }
+    }
+    // per-head rescale of the P.V accumulators
+#pragma unroll
+    for (int h = 0; h < kHeads; ++h) {
+        const float al = lane_f(alpha, head_lane(h));
+#pragma unroll
+        for (int d = 0; d < 4; ++d) acc[h][d] *= al;
+    }
+    wave_sync();
+    // P.V over token pairs
+#pragma unroll
+    for (int stp = 0; stp < kTile / 4; ++stp) {
+        const int pr = 2 * stp + ro.ph;
+        const uint2 va = *reinterpret_cast<const uint2 *>(reinterpret_cast<const char *>(&wt.v[2 * pr][0]) + ro.pd * 8);
+        const uint2 vb =
+            *reinterpret_cast<const uint2 *>(reinterpret_cast<const char *>(&wt.v[2 * pr + 1][0]) + ro.pd * 8);
+        const uint4 pp = wt.p[pr];
+        const uint32_t vv[4] = {__builtin_amdgcn_perm(vb.x, va.x, 0x05040100u),
+                                __builtin_amdgcn_perm(vb.x, va.x, 0x07060302u),
+                                __builtin_amdgcn_perm(vb.y, va.y, 0x05040100u),
+                                __builtin_amdgcn_perm(vb.y, va.y, 0x07060302u)};
+        const uint32_t pq[4] = {pp.x, pp.y, pp.z, pp.w};
+#pragma unroll
+        for (int h = 0; h < kHeads; ++h)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) acc[h][d] = dot2<DT>(pq[h], vv[d], acc[h][d]);
+    }
+    wave_sync();
+}
+
+// Reduce this wave's state to per-head values: m[h], den[h] (uniform) and acc
+// summed over the two P.V halves (valid in lanes < 32).
+__device__ __forceinline__ void wave_state(float m_l, float den_l, float (&acc)[kHeads][4], float (&mh)[kHeads],
+                                           float (&dh)[kHeads]) {
+#pragma unroll
+    for (int h = 0; h < kHeads; ++h)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) acc[h][d] += __shfl_xor(acc[h][d], 32, 64);
+    float dl = den_l;  // sum over the 8 token groups sharing this lane's head
+    dl += dpp<kRowRor8>(dl);
+    dl += __shfl_xor(dl, 16, 64);
+    dl += __shfl_xor(dl, 32, 64);
+#pragma unroll
+    for (int h = 0; h < kHeads; ++h) {
+        mh[h] = lane_f(m_l, head_lane(h));
+        dh[h] = lane_f(dl, head_lane(h));
+    }
+}
+
+}  // namespace valu
+}  // namespace sgd

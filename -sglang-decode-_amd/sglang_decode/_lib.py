@@ -14,7 +14,7 @@ from ._build import LIB_PATH
 
 SGD_EINVAL = -22
 SGD_BF16, SGD_FP16 = 0, 1
-KERNELS = {"auto": 0, "generic": 1, "valu": 2, "mfma": 3}
+KERNELS = {"auto": 0, "generic": 1, "valu": 2, "mfma": 3, "stream": 4}
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int32

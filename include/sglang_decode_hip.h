@@ -35,10 +35,11 @@ enum sgd_dtype { SGD_BF16 = 0, SGD_FP16 = 1 };
 
 /* Attention kernel selection (sgd_decode_args.kernel). */
 enum sgd_kernel {
-    SGD_KERNEL_AUTO = 0,     /* pick by geometry: MFMA for group >= 8, VALU for group <= 4 */
+    SGD_KERNEL_AUTO = 0,     /* pick by geometry and worker count (see sgd_persistent_decode) */
     SGD_KERNEL_GENERIC = 1,  /* any strides/alignment, any supported geometry */
-    SGD_KERNEL_VALU = 2,     /* LDS-staged K tile, wave64 DPP reductions, dot2 (group <= 4) */
-    SGD_KERNEL_MFMA = 3      /* MFMA QK^T and PV (group >= 8) */
+    SGD_KERNEL_VALU = 2,     /* per-task VALU kernel: LDS-staged K/V tiles, DPP reductions, dot2 (group <= 4) */
+    SGD_KERNEL_MFMA = 3,     /* MFMA QK^T and PV (group >= 8) */
+    SGD_KERNEL_STREAM = 4    /* VALU tile math, one workgroup per CU streaming tiles across tasks (group <= 4) */
 };
 
 /* Human-readable description of the last SGD_EINVAL / launch failure (thread-local). */
