@@ -41,7 +41,10 @@ int device_cus() {
 
 }  // namespace
 
-extern "C" int sgd_persistent_decode(const sgd_decode_args *args, void *stream) {
+namespace {
+
+// Host checks of the launch geometry; SGD_EINVAL (with the reason) or 0.
+int check_args(const sgd_decode_args *args) {
     if (!args) return einval("persistent_decode: null args");
     const sgd_decode_args &a = *args;
     if (a.kv_heads <= 0 || a.query_heads <= 0 || a.query_heads % a.kv_heads != 0)
@@ -56,29 +59,54 @@ extern "C" int sgd_persistent_decode(const sgd_decode_args *args, void *stream) 
     if (a.csr && (a.page_size != 1 || !a.indptr)) return einval("persistent_decode: CSR needs page_size 1 + indptr");
     if (!a.q || !a.k || !a.v || !a.pages || !a.partial || !a.lse || !a.counter)
         return einval("persistent_decode: null buffer");
-    const bool vec = vector_layout(a);
-    clear_stale_error();
+    return 0;
+}
+
+// The kernel a launch with these arguments runs (enum sgd_kernel), or SGD_EINVAL.
+int resolve_kernel(const sgd_decode_args &a) {
     switch (a.kernel) {
         case SGD_KERNEL_AUTO:
             // The stream kernel is one 1024-thread workgroup per CU: with more workers
             // than CUs they would run in turns, so the two-per-CU kernel takes over.
-            if (stream_supported(a) && a.workers <= device_cus())
-                return launch_attention_stream(a, (hipStream_t)stream);
-            if (valu_supported(a)) return launch_attention_valu(a, (hipStream_t)stream);
-            return launch_attention_generic(a, vec, (hipStream_t)stream);
+            if (stream_supported(a) && a.workers <= device_cus()) return SGD_KERNEL_STREAM;
+            if (valu_supported(a)) return SGD_KERNEL_VALU;
+            return SGD_KERNEL_GENERIC;
         case SGD_KERNEL_GENERIC:
-            return launch_attention_generic(a, vec, (hipStream_t)stream);
+            return SGD_KERNEL_GENERIC;
         case SGD_KERNEL_VALU:
             if (!valu_supported(a))
                 return einval("persistent_decode: the VALU kernel needs group <= 4, head_dim 128, unit dim "
                               "stride, 16-byte aligned rows and a power-of-two page size");
-            return launch_attention_valu(a, (hipStream_t)stream);
+            return SGD_KERNEL_VALU;
         case SGD_KERNEL_STREAM:
             if (!stream_supported(a))
                 return einval("persistent_decode: the stream kernel needs group <= 4, head_dim 128, unit dim "
                               "stride, 16-byte aligned rows and partial, and a power-of-two page size");
-            return launch_attention_stream(a, (hipStream_t)stream);
+            return SGD_KERNEL_STREAM;
         default:
             return einval("persistent_decode: kernel %d not available", a.kernel);
+    }
+}
+
+}  // namespace
+
+extern "C" int sgd_attention_kernel(const sgd_decode_args *args) {
+    if (int rc = check_args(args)) return rc;
+    return resolve_kernel(*args);
+}
+
+extern "C" int sgd_persistent_decode(const sgd_decode_args *args, void *stream) {
+    if (int rc = check_args(args)) return rc;
+    const sgd_decode_args &a = *args;
+    const int kernel = resolve_kernel(a);
+    if (kernel < 0) return kernel;
+    clear_stale_error();
+    switch (kernel) {
+        case SGD_KERNEL_STREAM:
+            return launch_attention_stream(a, (hipStream_t)stream);
+        case SGD_KERNEL_VALU:
+            return launch_attention_valu(a, (hipStream_t)stream);
+        default:
+            return launch_attention_generic(a, vector_layout(a), (hipStream_t)stream);
     }
 }

@@ -2,19 +2,20 @@
 // normalized partial outputs of its splits (kernels/merge.py:7-30).
 //
 // One wave per (request, head).  The merge is latency-bound (a few KB per row),
-// so nothing waits on a dependent chain: the split LSEs are loaded one per lane
-// in a single access, the global max and the weights exp(lse_s - max) come from
-// wave reductions, and the partial rows (each a coalesced 256-1024 B burst, lanes
-// owning head_dim/64 consecutive dims) are then streamed with independent loads.
-// This is the two-pass form of the reference's running-max merge (same value up
-// to rounding).  Rows with no split produce exact zeros (0 / max(den, 1e-30)); a
-// plan error produces NaN.
+// so the dependent chain is two memory round trips: the split count, then the
+// split LSEs (one per lane) together with up to kRowsInFlight partial rows
+// (each a coalesced 256-1024 B burst, lanes owning head_dim/64 consecutive dims),
+// all issued before any is used.  The global max and the weights exp(lse_s - max)
+// come from wave reductions.  This is the two-pass form of the reference's
+// running-max merge (same value up to rounding).  Rows with no split produce
+// exact zeros (0 / max(den, 1e-30)); a plan error produces NaN.
 #include "common.h"
 
 namespace sgd {
 namespace {
 
 constexpr int kMergeWaves = 4;
+constexpr int kRowsInFlight = 16;  // divides 64: a block of rows never straddles two LSE blocks
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <int DPL>
@@ -42,27 +43,41 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge(const float *__restr
     const int head = blockIdx.y * kMergeWaves + (threadIdx.x >> 6);
     const int r = blockIdx.x;
     if (head >= hq) return;
-    const int32_t n = counts[r];
+    const int32_t n = __builtin_amdgcn_readfirstlane(counts[r]);
     const int64_t row = (int64_t)r * hq + head;
     const float *lrow = lse + row * smax;
-    float mx = -INFINITY;
-    for (int b = 0; b < n; b += 64)
-        mx = fmaxf(mx, wave_max(b + lane < n ? lrow[b + lane] * kLog2e : -INFINITY));
+    const float *prow = partial + row * smax * D + lane * DPL;
     float den = 0.f, acc[DPL];
 #pragma unroll
     for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
-    const float *prow = partial + row * smax * D + lane * DPL;
-    for (int b = 0; b < n; b += 64) {
-        const float w = b + lane < n ? __builtin_amdgcn_exp2f(lrow[b + lane] * kLog2e - mx) : 0.f;
-        den += wave_sum(w);
-        const int cnt = min(64, n - b);
-#pragma unroll 4
-        for (int s = 0; s < cnt; ++s) {
-            const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
-            float v[DPL];
-            load_row<DPL>(prow + (int64_t)(b + s) * D, v);
+    float mx = -INFINITY;
+    if (n > 64) {  // more splits than lanes: the max first, over all of them
+        for (int b = 0; b < n; b += 64)
+            mx = fmaxf(mx, wave_max(b + lane < n ? lrow[b + lane] * kLog2e : -INFINITY));
+    }
+    for (int b = 0; b < n; b += kRowsInFlight) {
+        // rows b .. b+kRowsInFlight-1 and (per 64 rows) their LSEs, all in flight at once
+        float v[kRowsInFlight][DPL];
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) acc[i] += v[i] * ws;
+        for (int s = 0; s < kRowsInFlight; ++s) {
+            if (b + s < n) load_row<DPL>(prow + (int64_t)(b + s) * D, v[s]);
+            else
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) v[s][i] = 0.f;
+        }
+        const int lb = b & ~63;  // LSE block holding rows b..: lane l has split lb + l
+        const float l2 = lb + lane < n ? lrow[lb + lane] * kLog2e : -INFINITY;
+        if (n <= 64 && b == 0) mx = wave_max(l2);
+        const float w = lb + lane < n ? __builtin_amdgcn_exp2f(l2 - mx) : 0.f;
+        if ((b & 63) == 0) den += wave_sum(w);
+#pragma unroll
+        for (int s = 0; s < kRowsInFlight; ++s) {
+            if (b + s < n) {
+                const float ws = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), (b + s - lb)));
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) acc[i] += v[s][i] * ws;
+            }
         }
     }
     const bool bad = *error != 0;

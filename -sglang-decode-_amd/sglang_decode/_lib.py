@@ -15,6 +15,7 @@ from ._build import LIB_PATH
 SGD_EINVAL = -22
 SGD_BF16, SGD_FP16 = 0, 1
 KERNELS = {"auto": 0, "generic": 1, "valu": 2, "mfma": 3, "stream": 4}
+KERNEL_NAMES = {v: k for k, v in KERNELS.items()}
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int32
@@ -50,6 +51,7 @@ _SIGNATURES = {
     "sgd_greedy_lists": (_I, [_P] * 5 + [_I] * 3 + [_P]),
     "sgd_build_plan": (_I, [ctypes.POINTER(PlanBuffersC), _I, _I, _P, _I, _P]),
     "sgd_persistent_decode": (_I, [ctypes.POINTER(DecodeArgsC), _P]),
+    "sgd_attention_kernel": (_I, [ctypes.POINTER(DecodeArgsC)]),
     "sgd_merge_splits": (_I, [_P] * 6 + [_I] * 5 + [_P]),
     "sgd_host_static_lists": (_I, [_P, _I, _I, _I, _I, _P, _P]),
 }

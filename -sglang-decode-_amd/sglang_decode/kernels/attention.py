@@ -38,3 +38,4 @@ def persistent_decode(plan, layer, q, k, v, pages, indptr, scale, k_strides, v_s
     a.kernel = _lib.KERNELS[kernel] if isinstance(kernel, str) else int(kernel)
     check(_lib.lib().sgd_persistent_decode(ctypes.byref(a), _lib.stream_handle(q.device)),
           "persistent_decode")
+    return _lib.KERNEL_NAMES[_lib.lib().sgd_attention_kernel(ctypes.byref(a))]

@@ -47,7 +47,26 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-check", action="store_true")
     ap.add_argument("--json-out", default="")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="also run a plain N-MiB read+write kernel 5 times, so a rocprofv3 --pmc "
+                         "FETCH_SIZE / WRITE_SIZE pass can scale its counts to bytes")
+    ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "traffic_persistent_decode.json"),
+                    help="measured HBM bytes per attention launch (from rocprofv3 --pmc), used for "
+                         "roofline.traffic when kernel, schedule and workers match this run")
     return ap.parse_args()
+
+
+def measured_traffic(path, kernel, schedule, workers):
+    """HBM bytes per launch recorded from rocprofv3 FETCH_SIZE/WRITE_SIZE passes, or None."""
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for row in rec.get("launches", []):
+        if (row.get("kernel"), row.get("schedule"), row.get("workers")) == (kernel, schedule, workers):
+            return row.get("traffic_bytes")
+    return None
 
 
 def main():
@@ -165,11 +184,24 @@ def main():
     durs = [a.elapsed_time(b) * 1000.0 for a, b in ev[len(ev) // 10:]]
     kern_us = statistics.mean(durs)
     achieved = bytes_per_layer / (kern_us * 1e-6) / 1e9
+    kernel_name = engine.attention_kernel_name()
     roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                    frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None,
+                    frac=round(achieved / PEAK_HBM_GBS, 4),
+                    traffic=measured_traffic(args.traffic_file, kernel_name, best, workers),
+                    attention_kernel=kernel_name,
                     kernel="persistent_decode", kernel_us=round(kern_us, 2),
                     algorithmic_bytes=bytes_per_layer)
     print(f"[bench] attention kernel alone ({best}): {kern_us:.2f} us  {achieved:.0f} GB/s", flush=True)
+
+    if args.copy_calibration_mib:
+        # a plain copy kernel of known size: N MiB read + N MiB written per launch
+        n = args.copy_calibration_mib * (1 << 20) // 2
+        a = torch.randn(n, device=dev).to(torch.bfloat16)
+        b = torch.empty_like(a)
+        for _ in range(5):
+            torch.mul(a, 1, out=b)
+        torch.cuda.synchronize()
+        print(f"[bench] copy calibration: 5 x {args.copy_calibration_mib} MiB read+write", flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:

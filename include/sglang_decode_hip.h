@@ -151,6 +151,14 @@ typedef struct sgd_decode_args {
 int sgd_persistent_decode(const sgd_decode_args *args, void *stream);
 
 /*
+ * The attention kernel (enum sgd_kernel, never AUTO) that sgd_persistent_decode
+ * runs for these arguments, or SGD_EINVAL.  No reference counterpart: the
+ * reference has one Triton kernel; this reports which gfx950 kernel serves a
+ * launch (benchmarks and profiles name it).  Reads no device memory.
+ */
+int sgd_attention_kernel(const sgd_decode_args *args);
+
+/*
  * Split merge.  Replaces kernels/merge.py:7-30 (merge_splits), launched at
  * runtime/engine.py:71-73.  For every (r < bcap, h): LSE-weighted merge of the
  * counts[r] partials in split order; rows with counts[r] == 0 get 0; *error != 0

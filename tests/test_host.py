@@ -172,6 +172,32 @@ def test_abi_rejects_bad_arguments_before_launch():
         _lib.check(-22, "x")
 
 
+def test_attention_kernel_selection_is_host_only():
+    """sgd_attention_kernel answers from the arguments alone (no device access):
+    forced kernels are validated against the geometry they need."""
+    from sglang_decode import _lib
+    lib = _lib.lib()
+    args = _lib.DecodeArgsC()
+    # fake, aligned, never-dereferenced addresses: the query reads no memory
+    for name in ("q", "k", "v", "pages", "partial", "lse", "counter", "indptr"):
+        setattr(args, name, 1 << 20)
+    args.query_heads, args.kv_heads, args.head_dim = 32, 8, 128
+    args.max_splits, args.page_size, args.csr, args.workers = 16, 1, 1, 256
+    args.k_stride[:] = [1024, 0, 128, 1]
+    args.v_stride[:] = [1024, 0, 128, 1]
+    for forced in ("generic", "valu", "stream"):
+        args.kernel = _lib.KERNELS[forced]
+        assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == forced
+    args.query_heads = 64  # group 8: no VALU / stream kernel
+    for forced in ("valu", "stream"):
+        args.kernel = _lib.KERNELS[forced]
+        assert lib.sgd_attention_kernel(ctypes.byref(args)) == -22
+        assert b"group <= 4" in lib.sgd_last_error()
+    args.query_heads, args.kernel = 32, _lib.KERNELS["stream"]
+    args.partial = (1 << 20) + 4  # the stream kernel stores partial rows 16 bytes at a time
+    assert lib.sgd_attention_kernel(ctypes.byref(args)) == -22
+
+
 # ------------------------------------------------------------------ engine host validation
 
 def test_engine_validates_before_launch():
