@@ -56,15 +56,18 @@ def parse():
     return ap.parse_args()
 
 
-def measured_traffic(path, kernel, schedule, workers):
-    """HBM bytes per launch recorded from rocprofv3 FETCH_SIZE/WRITE_SIZE passes, or None."""
+def measured_traffic(path, kernel, workers, algorithmic_bytes):
+    """HBM bytes per launch recorded from rocprofv3 FETCH_SIZE/WRITE_SIZE passes for this
+    kernel, worker count and workload (same algorithmic bytes), or None.  The schedule only
+    changes which worker reads which rows, not the bytes, so it is not part of the key."""
     try:
         with open(path) as f:
             rec = json.load(f)
     except (OSError, ValueError):
         return None
     for row in rec.get("launches", []):
-        if (row.get("kernel"), row.get("schedule"), row.get("workers")) == (kernel, schedule, workers):
+        if (row.get("kernel"), row.get("workers"), row.get("algorithmic_bytes")) == (
+                kernel, workers, algorithmic_bytes):
             return row.get("traffic_bytes")
     return None
 
@@ -187,7 +190,7 @@ def main():
     kernel_name = engine.attention_kernel_name()
     roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
                     frac=round(achieved / PEAK_HBM_GBS, 4),
-                    traffic=measured_traffic(args.traffic_file, kernel_name, best, workers),
+                    traffic=measured_traffic(args.traffic_file, kernel_name, workers, bytes_per_layer),
                     attention_kernel=kernel_name,
                     kernel="persistent_decode", kernel_us=round(kern_us, 2),
                     algorithmic_bytes=bytes_per_layer)
