@@ -40,7 +40,7 @@ using namespace valu;
 constexpr int kComputeWaves = 15;
 constexpr int kThreads = 64 * (kComputeWaves + 1);
 constexpr int kRing = 10;
-constexpr int kQueueTiles = 32;
+constexpr int kQueueTiles = 16;
 constexpr int32_t kNotYet = -2;  // the tile lies past every published task
 constexpr int32_t kNone = -1;    // the task stream ended before the tile
 constexpr int32_t kFar = 0x7fffffff;
@@ -270,6 +270,13 @@ __device__ void compute_wave(StreamShared &sh, const sgd_decode_args &a, int wav
         for (int d = 0; d < 4; ++d) acc[h][d] = 0.f;
     int32_t cnt = 0;
 
+    // Reserves the tile after the one just issued (in task kx) and prefetches its indices.
+    auto reserve_after = [&](int32_t kx) -> int32_t {
+        const int32_t x = grab_tile(sh, lane);
+        prefetch_index(x, kx);
+        return x;
+    };
+
     for (;;) {
         int lane_v = lane;
         asm volatile("" : "+v"(lane_v));
@@ -278,12 +285,11 @@ __device__ void compute_wave(StreamShared &sh, const sgd_decode_args &a, int wav
         tile_stage(wt, kr, vr, lane_v, nvalid);
         int32_t kscan = kc;
         int32_t kn = find_task(sh, gn, kscan);
-        int32_t gnn = 0;
+        int32_t gnn = -1;
         const bool issued = kn >= 0;
         if (issued) {
             issue(gn, kn, have_idx);
-            gnn = grab_tile(sh, lane);
-            prefetch_index(gnn, kn);
+            gnn = reserve_after(kn);
         }
         wave_sync();
         tile_compute<DT>(wt, sc.q, nvalid, scale2, Roles(lane_v), m_l, den_l, acc);
@@ -306,8 +312,7 @@ __device__ void compute_wave(StreamShared &sh, const sgd_decode_args &a, int wav
             }
             if (kn == kNone) break;
             issue(gn, kn, false);
-            gnn = grab_tile(sh, lane);
-            prefetch_index(gnn, kn);
+            gnn = reserve_after(kn);
         }
         lds_release(&sh.pos[wave], kn, lane);
         kc = kn;
