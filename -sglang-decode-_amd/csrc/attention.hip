@@ -7,8 +7,10 @@ namespace sgd {
 int launch_attention_generic(const sgd_decode_args &a, bool vec, hipStream_t stream);
 int launch_attention_valu(const sgd_decode_args &a, hipStream_t stream);
 int launch_attention_stream(const sgd_decode_args &a, hipStream_t stream);
+int launch_attention_mfma(const sgd_decode_args &a, hipStream_t stream);
 bool valu_supported(const sgd_decode_args &a);
 bool stream_supported(const sgd_decode_args &a);
+bool mfma_supported(const sgd_decode_args &a);
 }
 
 using namespace sgd;
@@ -70,6 +72,7 @@ int resolve_kernel(const sgd_decode_args &a) {
             // than CUs they would run in turns, so the two-per-CU kernel takes over.
             if (stream_supported(a) && a.workers <= device_cus()) return SGD_KERNEL_STREAM;
             if (valu_supported(a)) return SGD_KERNEL_VALU;
+            if (mfma_supported(a)) return SGD_KERNEL_MFMA;
             return SGD_KERNEL_GENERIC;
         case SGD_KERNEL_GENERIC:
             return SGD_KERNEL_GENERIC;
@@ -78,6 +81,11 @@ int resolve_kernel(const sgd_decode_args &a) {
                 return einval("persistent_decode: the VALU kernel needs group <= 4, head_dim 128, unit dim "
                               "stride, 16-byte aligned rows and a power-of-two page size");
             return SGD_KERNEL_VALU;
+        case SGD_KERNEL_MFMA:
+            if (!mfma_supported(a))
+                return einval("persistent_decode: the MFMA kernel needs group 8 or 16, head_dim 128, unit dim "
+                              "stride, 16-byte aligned rows and a power-of-two page size");
+            return SGD_KERNEL_MFMA;
         case SGD_KERNEL_STREAM:
             if (!stream_supported(a))
                 return einval("persistent_decode: the stream kernel needs group <= 4, head_dim 128, unit dim "
@@ -106,6 +114,8 @@ extern "C" int sgd_persistent_decode(const sgd_decode_args *args, void *stream) 
             return launch_attention_stream(a, (hipStream_t)stream);
         case SGD_KERNEL_VALU:
             return launch_attention_valu(a, (hipStream_t)stream);
+        case SGD_KERNEL_MFMA:
+            return launch_attention_mfma(a, (hipStream_t)stream);
         default:
             return launch_attention_generic(a, vector_layout(a), (hipStream_t)stream);
     }

@@ -1,0 +1,325 @@
+// Persistent paged GQA decode attention for query-head groups of 8 or 16 heads
+// (Llama-3-70B: 64 q / 8 kv), head_dim 128, unit dim stride -- the MFMA path.
+//
+// With 8-16 query heads per KV head, QK^T and P.V are real (if small) matrix
+// products, so both run on the matrix cores with v_mfma_f32_16x16x32_{bf16,f16}
+// (fp32 accumulate); the online softmax stays in fp32 on the VALU.  Lane l of a
+// wave is (m, j) = (l % 16, l / 16).  Operand layouts of the 16x16x32 MFMA:
+// A[m][8j .. 8j+7], B[8j .. 8j+7][n = l % 16], D[4j + i][n = l % 16].
+//
+// A 32-token tile of one (record, kv head) per wave, two halves of 16 tokens:
+//   S^T = K . Q^T   (M = 16 tokens of a half, N = 16 padded heads, K = 128 dims in
+//                    four 32-dim chunks): lane (m, j) loads the 16 bytes of token m's
+//                    K row at dims 32c + 8j .. +7 straight into the A operand; the
+//                    group's q rows are the B operand, held in registers per task.
+//                    Output: lane (n, j) has S[head n][token 16h + 4j + i].
+//   softmax        per head n, over the 8 scores of each lane and the 4 lanes
+//                    (j = 0..3) of the head's column; P rounded to the KV dtype
+//                    (kernels/attention.py:78).
+//   O^T += V^T . P^T (M = 16, N = heads, K = 32 tokens): the B operand is P
+//                    exactly as S^T left it (k slot s of lane group j = token
+//                    4j + s for s < 4, 16 + 4j + s - 4 otherwise), so P never
+//                    moves.  The A operand needs, per lane, one dim of those 8
+//                    tokens: lane (m, j) loads the 16 bytes at dims 8m .. 8m+7 of
+//                    each of the 8 tokens (16 lanes cover a 256 B V row), and MFMA
+//                    block b (0..7) takes element b of each -- output row r of
+//                    block b is dim 8r + b.  No LDS transpose, just v_perm_b32.
+// Output: lane (n, j) accumulates head n, dims 32j .. 32j+31.
+//
+// Worker = one workgroup of 4 waves (two per CU); tiles of a task are dealt to the
+// waves round-robin, each wave double-buffers its next tile's K/V loads in
+// registers, and at the end of the task the waves' (m, den, O) are merged through
+// LDS into the partial rows and natural-log LSEs of slot (request, head, split)
+// (kernels/attention.py:81-84).  Tasks and their order come from
+// attention_common.h's dispatch.
+#include "valu_ops.h"
+
+namespace sgd {
+namespace {
+
+using valu::uni;
+
+constexpr int kWaves = 4;
+constexpr int kTileT = 32;     // tokens per tile
+constexpr int kD = 128;
+constexpr int kHeadsM = 16;    // MFMA N: query heads, padded
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct MfmaShared {
+    float o[kWaves][kHeadsM][kD];  // per-wave unnormalized outputs, 32 KB
+    float m[kWaves][kHeadsM];
+    float d[kWaves][kHeadsM];
+    int32_t cursor;
+};
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
+    if constexpr (DT == SGD_BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                       0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                      0, 0);
+}
+
+// Token (0..31 within the tile) of k slot s for lane group j (the P / V^T order).
+__device__ __forceinline__ int slot_token(int j, int s) { return s < 4 ? 4 * j + s : 16 + 4 * j + (s - 4); }
+
+struct TileRegs {
+    uint4 k[2][4];  // [half][dim chunk]: token 16h + m, dims 32c + 8j .. +7
+    uint4 v[8];     // [k slot]: token slot_token(j, s), dims 8m .. 8m+7
+};
+
+struct Src {
+    const char *kbase, *vbase;
+    int64_t kp, kt, vp, vt;
+    int32_t request, ind0, start, end, page_shift, page_mask;
+};
+
+// lane l < 32 fetches the physical page / slot index of token tok0 + l (0 past `end`,
+// which addresses an in-bounds row).
+template <bool CSR>
+__device__ __forceinline__ int32_t tile_index(const sgd_decode_args &a, const Src &t, int32_t tok0, int lane) {
+    const int32_t tok = tok0 + lane;
+    int32_t v = 0;
+    if (lane < kTileT && tok < t.end) {
+        if constexpr (CSR) v = a.pages[t.ind0 + tok];
+        else v = a.pages[(int64_t)t.request * a.pt_stride[0] + (int64_t)(tok >> t.page_shift) * a.pt_stride[1]];
+    }
+    return v;
+}
+
+// All 16 loads are unconditional, so nothing branches between a tile's loads and
+// the compute that overlaps them.
+template <bool CSR>
+__device__ __forceinline__ void tile_issue(const Src &t, int32_t tok0, int32_t idxv, int lane, TileRegs &r) {
+    const int m = lane & 15, j = lane >> 4;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int tt = 16 * h + m;
+        const uint32_t phys = (uint32_t)__shfl(idxv, tt, 64);
+        int64_t off = (int64_t)phys * t.kp;
+        if constexpr (!CSR) off += (int64_t)((tok0 + tt) & t.page_mask) * t.kt;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            r.k[h][c] = *reinterpret_cast<const uint4 *>(t.kbase + off + (32 * c + 8 * j) * 2);
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const int tt = slot_token(j, s);
+        const uint32_t phys = (uint32_t)__shfl(idxv, tt, 64);
+        int64_t off = (int64_t)phys * t.vp + m * 16;
+        if constexpr (!CSR) off += (int64_t)((tok0 + tt) & t.page_mask) * t.vt;
+        r.v[s] = *reinterpret_cast<const uint4 *>(t.vbase + off);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) { return valu::pack2<DT>(lo, hi); }
+
+// One tile: S^T, online softmax (exp2 domain), O^T += V^T P^T.  m_l / den_l are this
+// lane's head's running max and partial denominator (its own 8 tokens per tile).
+template <int DT>
+__device__ __forceinline__ void tile_compute(TileRegs &r, const uint4 (&q)[4], int32_t nvalid, float scale2,
+                                             int lane, float &m_l, float &den_l, f32x4 (&o)[8]) {
+    const int j = lane >> 4;
+    f32x4 s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        s[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s[h] = mfma<DT>(r.k[h][c], q[c], s[h]);
+    }
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int tt = slot_token(j, i);  // s[i / 4][i % 4] is token 16 (i / 4) + 4j + i % 4
+        x[i] = tt < nvalid ? s[i >> 2][i & 3] * scale2 : -INFINITY;
+    }
+    if (nvalid < kTileT) {  // rows past the task's end: zero V (their p is exactly zero)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (slot_token(j, i) >= nvalid) r.v[i] = make_uint4(0, 0, 0, 0);
+    }
+    float mx = x[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, x[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_l, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m_l - m_new);
+    m_l = m_new;
+    float p[8], ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        p[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+        ps += p[i];
+    }
+    den_l = den_l * alpha + ps;
+    const uint4 pb = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]), pack2<DT>(p[4], p[5]),
+                                pack2<DT>(p[6], p[7]));
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        // A operand of block b: element b (dim 8m + b) of the 8 slot tokens' V chunks
+        const int dw = b >> 1;
+        const uint32_t sel = (b & 1) ? 0x07060302u : 0x05040100u;
+        auto e = [&](int s) { return (&r.v[s].x)[dw]; };
+        const uint4 av = make_uint4(__builtin_amdgcn_perm(e(1), e(0), sel), __builtin_amdgcn_perm(e(3), e(2), sel),
+                                    __builtin_amdgcn_perm(e(5), e(4), sel), __builtin_amdgcn_perm(e(7), e(6), sel));
+        o[b] = o[b] * alpha;
+        o[b] = mfma<DT>(av, pb, o[b]);
+    }
+}
+
+template <int DT, bool CSR>
+__global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_args a) {
+    extern __shared__ __align__(16) char dyn_smem[];
+    MfmaShared &sh = *reinterpret_cast<MfmaShared *>(dyn_smem);
+    const int lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
+    const int32_t G = a.query_heads / a.kv_heads;
+    const float scale2 = a.scale * kLog2e;
+
+    for_each_task(a, &sh.cursor, [&](int32_t task, int32_t mode) {
+        const TaskInfo ti = decode_task(a, task, mode);
+        Src t;
+        t.request = uni(ti.request);
+        t.start = uni(ti.start);
+        t.end = uni(ti.end);
+        const int32_t split = uni(ti.split), group = uni(ti.group);
+        t.ind0 = CSR ? uni(a.indptr[t.request]) : 0;
+        t.kbase = static_cast<const char *>(a.k) + group * (a.k_stride[2] * 2);
+        t.vbase = static_cast<const char *>(a.v) + group * (a.v_stride[2] * 2);
+        t.kp = a.k_stride[0] * 2;
+        t.kt = a.k_stride[1] * 2;
+        t.vp = a.v_stride[0] * 2;
+        t.vt = a.v_stride[1] * 2;
+        t.page_shift = __builtin_ctz((unsigned)a.page_size);
+        t.page_mask = a.page_size - 1;
+        const int32_t ntiles = (t.end - t.start + kTileT - 1) / kTileT;
+        const int32_t n0 = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
+
+        // q rows as the B operand: head n = lane % 16, dims 32c + 8j .. +7 (zero past G)
+        uint4 q[4];
+        {
+            const int n = lane & 15, j = lane >> 4;
+            const int64_t qd = a.q_stride[2];
+            const uint16_t *qp = static_cast<const uint16_t *>(a.q) + (int64_t)t.request * a.q_stride[0] +
+                                 (int64_t)(group * G + n) * a.q_stride[1];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                q[c] = make_uint4(0, 0, 0, 0);
+                if (n < G) {
+                    const uint16_t *p = qp + (int64_t)(32 * c + 8 * j) * qd;
+                    if (qd == 1 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+                        q[c] = *reinterpret_cast<const uint4 *>(p);
+                    } else {
+                        uint32_t w4[4] = {0, 0, 0, 0};
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) w4[e >> 1] |= (uint32_t)p[e * qd] << (16 * (e & 1));
+                        q[c] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+                    }
+                }
+            }
+        }
+
+        float m_l = -INFINITY, den_l = 0.f;
+        f32x4 o[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        if (n0 > 0) {
+            TileRegs cur, nxt;
+            int32_t tile = wave;
+            tile_issue<CSR>(t, t.start + tile * kTileT, tile_index<CSR>(a, t, t.start + tile * kTileT, lane), lane,
+                            cur);
+            // indices of the wave's next tile (clamped to its last one)
+            int32_t idx_next = tile_index<CSR>(a, t, t.start + min(tile + kWaves, ntiles - 1) * kTileT, lane);
+            for (int32_t e = 0; e + 1 < n0; ++e) {
+                const int32_t nt = tile + kWaves;
+                tile_issue<CSR>(t, t.start + nt * kTileT, idx_next, lane, nxt);
+                idx_next = tile_index<CSR>(a, t, t.start + min(nt + kWaves, ntiles - 1) * kTileT, lane);
+                tile_compute<DT>(cur, q, min(kTileT, t.end - (t.start + tile * kTileT)), scale2, lane, m_l, den_l,
+                                 o);
+                cur = nxt;
+                tile = nt;
+            }
+            tile_compute<DT>(cur, q, min(kTileT, t.end - (t.start + tile * kTileT)), scale2, lane, m_l, den_l, o);
+        }
+
+        // wave state to LDS: head n = lane % 16, dims 32j + 8i + b
+        den_l += __shfl_xor(den_l, 16, 64);
+        den_l += __shfl_xor(den_l, 32, 64);
+        __syncthreads();  // the previous task's combine is done reading shared memory
+        {
+            const int n = lane & 15, j = lane >> 4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float *dst = &sh.o[wave][n][32 * j + 8 * i];
+                *reinterpret_cast<float4 *>(dst) = make_float4(o[0][i], o[1][i], o[2][i], o[3][i]);
+                *reinterpret_cast<float4 *>(dst + 4) = make_float4(o[4][i], o[5][i], o[6][i], o[7][i]);
+            }
+            if (j == 0) {
+                sh.m[wave][n] = m_l;
+                sh.d[wave][n] = den_l;
+            }
+        }
+        __syncthreads();
+        for (int x = threadIdx.x; x < G * kD; x += 64 * kWaves) {
+            const int h = x / kD, d = x % kD;
+            float mm = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, sh.m[w][h]);
+            float dd = 0.f, acc = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const float sc = __builtin_amdgcn_exp2f(sh.m[w][h] - mm);
+                dd += sh.d[w][h] * sc;
+                acc += sh.o[w][h][d] * sc;
+            }
+            const int64_t slot = ((int64_t)t.request * a.query_heads + group * G + h) * a.max_splits + split;
+            a.partial[slot * kD + d] = acc / dd;
+            if (d == 0) a.lse[slot] = (mm + __log2f(dd)) * kLn2;
+        }
+    });
+}
+
+template <int DT, bool CSR>
+int launch_mfma_t(const sgd_decode_args &a, hipStream_t stream) {
+    static bool attr = false;
+    constexpr int bytes = (int)sizeof(MfmaShared);
+    if (!attr) {
+        if (hipFuncSetAttribute((const void *)k_attention_mfma<DT, CSR>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                bytes) != hipSuccess)
+            return einval("mfma attention: cannot reserve %d B of LDS", bytes);
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_attention_mfma<DT, CSR>), dim3(a.workers), dim3(64 * kWaves), bytes, stream, a);
+    return launch_status("persistent_decode(mfma)");
+}
+
+}  // namespace
+
+// Group 8 or 16, head_dim 128, unit dim stride, 16-byte aligned rows, power-of-two page.
+bool mfma_supported(const sgd_decode_args &a) {
+    const int g = a.query_heads / a.kv_heads;
+    if ((g != 8 && g != 16) || a.head_dim != kD) return false;
+    if (a.k_stride[3] != 1 || a.v_stride[3] != 1) return false;
+    if ((reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.v)) & 15) return false;
+    if (a.page_size & (a.page_size - 1)) return false;
+    for (int i = 0; i < 3; ++i)
+        if (a.k_stride[i] % 8 || a.v_stride[i] % 8) return false;
+    return a.k_stride[0] < (1ll << 40) && a.v_stride[0] < (1ll << 40);
+}
+
+int launch_attention_mfma(const sgd_decode_args &a, hipStream_t stream) {
+    if (a.dtype == SGD_BF16)
+        return a.csr ? launch_mfma_t<SGD_BF16, true>(a, stream) : launch_mfma_t<SGD_BF16, false>(a, stream);
+    return a.csr ? launch_mfma_t<SGD_FP16, true>(a, stream) : launch_mfma_t<SGD_FP16, false>(a, stream);
+}
+
+}  // namespace sgd

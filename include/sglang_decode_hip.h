@@ -38,7 +38,7 @@ enum sgd_kernel {
     SGD_KERNEL_AUTO = 0,     /* pick by geometry and worker count (see sgd_persistent_decode) */
     SGD_KERNEL_GENERIC = 1,  /* any strides/alignment, any supported geometry */
     SGD_KERNEL_VALU = 2,     /* per-task VALU kernel: LDS-staged K/V tiles, DPP reductions, dot2 (group <= 4) */
-    SGD_KERNEL_MFMA = 3,     /* MFMA QK^T and PV (group >= 8) */
+    SGD_KERNEL_MFMA = 3,     /* MFMA QK^T and PV, K/V straight from HBM into operands (group 8 or 16) */
     SGD_KERNEL_STREAM = 4    /* VALU tile math, one workgroup per CU streaming tiles across tasks (group <= 4) */
 };
 

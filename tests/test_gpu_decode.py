@@ -170,3 +170,45 @@ def test_stream_short_tasks_and_small_worker_counts(mode):
     engine = DecodeEngine(c, force_mode=mode, kernel="stream")
     out = run(engine, lengths, (q, k, v, indices), indptr=indptr)
     close(out[:len(lengths)], OA.csr_attention(q, k, v, indptr, indices, lengths)[:len(lengths)])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("mode", list(Mode))
+@pytest.mark.parametrize("hq", [64, 128])
+def test_mfma_kernel_groups_8_and_16_paged(hq, mode, dtype):
+    """Group 8 (Llama-3-70B heads) and 16 on the MFMA kernel: page 16, ragged lengths
+    (a 1-token request, a 31-token one that ends mid-tile, an empty row)."""
+    c = DecodeConfig(batch_capacity=6, max_splits=16, max_context=4096, query_heads=hq, kv_heads=8,
+                     head_dim=128, page_size=16, workers=64)
+    lengths = [4096, 1, 999, 31, 0, 2500]
+    inputs = W.make_inputs(c, lengths, seed=23, dtype=dtype)
+    engine = DecodeEngine(c, dtype=dtype, force_mode=mode, kernel="mfma")
+    out = run(engine, lengths, inputs, scale=0.07)
+    assert engine.attention_kernel_name() == "mfma"
+    close(out[:6], OA.paged_attention(*inputs[:3], inputs[3], lengths, c.page_size, scale=0.07))
+
+
+@pytest.mark.parametrize("mode", [Mode.R1, Mode.D1, Mode.STATIC])
+def test_mfma_kernel_csr(mode):
+    c = DecodeConfig(batch_capacity=8, max_splits=8, max_context=3000, query_heads=64, kv_heads=8,
+                     head_dim=128, page_size=1, workers=40)
+    lengths = [3000, 17, 640, 1, 2049, 0, 33, 700]
+    q, k, v, indptr, indices = W.make_csr_inputs(c, lengths, seed=29, pool_tokens=1 << 14)
+    engine = DecodeEngine(c, force_mode=mode)  # auto picks the MFMA kernel for group 8
+    out = run(engine, lengths, (q, k, v, indices), indptr=indptr)
+    assert engine.attention_kernel_name() == "mfma"
+    close(out[:8], OA.csr_attention(q, k, v, indptr, indices, lengths)[:8])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_llama70b_paged_shape_subset(dtype):
+    """The 70B paged configuration (page 16, 64 q / 8 kv, contexts in [2048, 16384]) on
+    the first 6 of its seeded requests."""
+    full = W.config_for("c4")
+    c = DecodeConfig(batch_capacity=6, max_splits=full.max_splits, max_context=full.max_context,
+                     query_heads=64, kv_heads=8, head_dim=128, page_size=16, workers=128)
+    lengths = W.c4_lengths()[:6]
+    inputs = W.make_inputs(c, lengths, seed=41, dtype=dtype)
+    engine = DecodeEngine(c, dtype=dtype, force_mode=Mode.D1)
+    out = run(engine, lengths, inputs)
+    close(out[:6], OA.paged_attention(*inputs[:3], inputs[3], lengths, c.page_size))
