@@ -83,7 +83,7 @@ int resolve_kernel(const sgd_decode_args &a) {
             return SGD_KERNEL_VALU;
         case SGD_KERNEL_MFMA:
             if (!mfma_supported(a))
-                return einval("persistent_decode: the MFMA kernel needs group 8 or 16, head_dim 128, unit dim "
+                return einval("persistent_decode: the MFMA kernel needs group <= 16, head_dim 128, unit dim "
                               "stride, 16-byte aligned rows and a power-of-two page size");
             return SGD_KERNEL_MFMA;
         case SGD_KERNEL_STREAM:

@@ -304,10 +304,11 @@ int launch_mfma_t(const sgd_decode_args &a, hipStream_t stream) {
 
 }  // namespace
 
-// Group 8 or 16, head_dim 128, unit dim stride, 16-byte aligned rows, power-of-two page.
+// Any group up to 16 (the padded MFMA N), head_dim 128, unit dim stride, 16-byte
+// aligned rows, power-of-two page.
 bool mfma_supported(const sgd_decode_args &a) {
     const int g = a.query_heads / a.kv_heads;
-    if ((g != 8 && g != 16) || a.head_dim != kD) return false;
+    if (g < 1 || g > kHeadsM || a.head_dim != kD) return false;
     if (a.k_stride[3] != 1 || a.v_stride[3] != 1) return false;
     if ((reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.v)) & 15) return false;
     if (a.page_size & (a.page_size - 1)) return false;

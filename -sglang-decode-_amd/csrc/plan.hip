@@ -34,25 +34,35 @@ struct PlanShared {
     int32_t bucket_packed_packs[kMaxBuckets];
     int32_t bucket_packed_tasks[kMaxBuckets];
     int32_t mode;
+    int32_t record_count;
     int32_t max_w, min_w;
     int32_t red_max[16], red_min[16];
 };
 
 // ---------------------------------------------------------------- count/scan
+// Optional LDS copies of the per-row values for the fused kernel's later stages.
+struct RowMirror {
+    int32_t *lengths, *counts, *offsets, *chunk;  // LDS, [bcap] ([bcap + 1] for offsets)
+};
+
+constexpr int kMaxRowsPerThread = 4;  // bcap <= 4096 = 4 x kPlanThreads
+
 __device__ void stage_count_scan(const int32_t *lengths, const int32_t *splits, const int32_t *active_p,
                                  int32_t *counts, int32_t *offsets, int32_t *chunk, int32_t *record_count,
                                  int32_t *error, int32_t bcap, int32_t smax, int32_t max_context,
-                                 PlanShared &sh) {
+                                 PlanShared &sh, const RowMirror *mirror = nullptr) {
     const int tid = threadIdx.x;
     const int per = (bcap + kPlanThreads - 1) / kPlanThreads;  // rows per thread (contiguous)
     const int32_t active = *active_p;
     const int r0 = tid * per;
     int invalid_any = 0;
-    int32_t local = 0;
+    int32_t local = 0, nrow[kMaxRowsPerThread];
     // pass 1: validity, chunk, n
-    for (int i = 0; i < per; ++i) {
+#pragma unroll
+    for (int i = 0; i < kMaxRowsPerThread; ++i) {
+        nrow[i] = 0;
         const int r = r0 + i;
-        if (r >= bcap) break;
+        if (i >= per || r >= bcap) continue;
         const bool live = r < active;
         const int32_t length = live ? lengths[r] : 0;
         const int32_t s = live ? splits[r] : 1;
@@ -60,34 +70,46 @@ __device__ void stage_count_scan(const int32_t *lengths, const int32_t *splits, 
         invalid_any |= invalid;
         const int32_t c = wmul(cdiv(cdiv(max(length, 0), max(s, 1)), 32), 32);
         chunk[r] = c;
-        const int32_t n = (live && !invalid) ? cdiv(length, max(c, 1)) : 0;
-        counts[r] = n;  // provisional; rewritten below if the batch is in error
-        local = wadd(local, n);
+        nrow[i] = (live && !invalid) ? cdiv(length, max(c, 1)) : 0;
+        local = wadd(local, nrow[i]);
+        if (mirror) {
+            mirror->lengths[r] = length;
+            mirror->chunk[r] = c;
+        }
     }
     const bool err = (active < 0) || (active > bcap) || __syncthreads_or(invalid_any);
     if (err) local = 0;
     int32_t total;
     int32_t running = block_exclusive_scan<int32_t>(local, sh.scan_tmp, &total);
-    for (int i = 0; i < per; ++i) {
+#pragma unroll
+    for (int i = 0; i < kMaxRowsPerThread; ++i) {
         const int r = r0 + i;
-        if (r >= bcap) break;
-        const int32_t n = err ? 0 : counts[r];
+        if (i >= per || r >= bcap) continue;
+        const int32_t n = err ? 0 : nrow[i];
         counts[r] = n;
         offsets[r] = running;
+        if (mirror) {
+            mirror->counts[r] = n;
+            mirror->offsets[r] = running;
+        }
         running = wadd(running, n);
     }
     if (tid == 0) {
         offsets[bcap] = total;
         *record_count = total;
         *error = err ? 1 : 0;
+        sh.record_count = total;
     }
 }
 
 // ---------------------------------------------------------------- records
+// lengths/counts/offsets/chunk are read through the given pointers (global memory for
+// the single-stage kernel, the LDS copies in the fused one); weight_mirror, when set, is
+// an LDS copy of the weights for the later stages.
 __device__ void stage_emit_records(const int32_t *lengths, const int32_t *counts, const int32_t *offsets,
                                    const int32_t *chunk, int32_t *request, int32_t *split, int32_t *begin,
                                    int32_t *end, int32_t *weight, int32_t bcap, int32_t smax,
-                                   int32_t block_kv) {
+                                   int32_t block_kv, int32_t *weight_mirror = nullptr) {
     const int64_t pairs = (int64_t)bcap * smax;
     for (int64_t p = threadIdx.x; p < pairs; p += kPlanThreads) {
         const int r = (int)(p / smax), s = (int)(p % smax);
@@ -101,7 +123,9 @@ __device__ void stage_emit_records(const int32_t *lengths, const int32_t *counts
         split[idx] = s;
         begin[idx] = b;
         end[idx] = e;
-        weight[idx] = cdiv(wadd(e, -b), block_kv);
+        const int32_t w = cdiv(wadd(e, -b), block_kv);
+        weight[idx] = w;
+        if (weight_mirror) weight_mirror[idx] = w;
     }
 }
 
@@ -112,13 +136,14 @@ __device__ __forceinline__ int bucket_of(int32_t w, int buckets) {
 }
 
 // ---------------------------------------------------------------- mode, order, packs
-__device__ void stage_order_and_packs(const int32_t *weight, const int32_t *record_count, int32_t *order,
+// weight is read through the given pointer (global, or the fused kernel's LDS copy);
+// total = record count.  Leaves the selected mode in sh.mode.
+__device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int32_t *order,
                                       int32_t *pack_first, int32_t *pack_count, int32_t *num_packs,
                                       int32_t *mode_out, const int32_t *rules, int32_t rule_count,
                                       int32_t force, int32_t hkv, int32_t workers, int32_t buckets,
                                       int32_t record_capacity, PlanShared &sh) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int32_t total = *record_count;
     const int per = (record_capacity + kPlanThreads - 1) / kPlanThreads;
     const int i0 = tid * per;
     // max/min weight over valid records (max starts at 1, min at INT32_MAX as plan.py:57-58)
@@ -163,25 +188,31 @@ __device__ void stage_order_and_packs(const int32_t *weight, const int32_t *reco
     // Stable partition by bucket, heaviest first.  Each thread owns a contiguous
     // segment; per-bucket counts are packed 4 x 16-bit per uint64 so four block
     // scans cover 16 buckets (segment counts <= 16, totals <= 16384 < 2^16).
+    // (arrays below are only ever indexed by compile-time constants: no scratch)
     uint64_t cnt[4] = {0, 0, 0, 0};
     for (int k = 0; k < per; ++k) {
         const int i = i0 + k;
         if (i >= total) break;
         const int b = bucket_of(weight[i], buckets);
-        cnt[b >> 2] += (uint64_t)1 << (16 * (b & 3));
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if ((b >> 2) == q) cnt[q] += (uint64_t)1 << (16 * (b & 3));
     }
     uint64_t base[4], tot[4];
+#pragma unroll
     for (int q = 0; q < 4; ++q) base[q] = block_exclusive_scan<uint64_t>(cnt[q], sh.scan_tmp64, &tot[q]);
     if (tid == 0) {
+#pragma unroll
+        for (int b = 0; b < kMaxBuckets; ++b)
+            sh.bucket_size[b] = (int32_t)((tot[b >> 2] >> (16 * (b & 3))) & 0xffff);
         int32_t rec_base = 0, pack_base = 0;
         for (int b = buckets - 1; b >= 0; --b) {
-            const int32_t size = (int32_t)((tot[b >> 2] >> (16 * (b & 3))) & 0xffff);
+            const int32_t size = sh.bucket_size[b];
             const int32_t tasks = size * hkv;
             const int32_t width = (mode == 4) ? min(4, max(1, max_w / (1 << b))) : 1;
             const int32_t packed_tasks = max(0, tasks - workers) / width * width;
             const int32_t packed_packs = packed_tasks / width;
             const int32_t count = packed_packs + tasks - packed_tasks;
-            sh.bucket_size[b] = size;
             sh.bucket_record_base[b] = rec_base;
             sh.bucket_pack_base[b] = pack_base;
             sh.bucket_pack_count[b] = count;
@@ -195,6 +226,7 @@ __device__ void stage_order_and_packs(const int32_t *weight, const int32_t *reco
     }
     __syncthreads();
     int32_t rank[kMaxBuckets];
+#pragma unroll
     for (int b = 0; b < kMaxBuckets; ++b) rank[b] = (int32_t)((base[b >> 2] >> (16 * (b & 3))) & 0xffff);
     for (int k = 0; k < per; ++k) {
         const int i = i0 + k;
@@ -232,12 +264,18 @@ struct GreedyShared {
     int32_t tail[kGreedyMaxWorkers];
 };
 
-__device__ void stage_greedy_lists(const int32_t *weight, const int32_t *record_count, const int32_t *mode_p,
+// keys / load / tail are LDS arrays of kGreedyMaxRecords / workers entries.  weight may
+// alias keys (the fused kernel's LDS weights become the keys in place: each index is
+// read and then written by the same thread).
+__device__ void stage_greedy_lists(const int32_t *weight, int32_t total, int32_t mode,
                                    int32_t *static_head, int32_t *static_next, int32_t hkv,
-                                   int32_t workers, GreedyShared &g) {
-    if (*mode_p != 2) return;
+                                   int32_t workers, uint32_t *keys, int32_t *load, int32_t *tail) {
+    struct {
+        uint32_t *keys;
+        int32_t *load, *tail;
+    } g{keys, load, tail};
+    if (mode != 2) return;
     const int tid = threadIdx.x, lane = tid & 63;
-    const int32_t total = *record_count;
     int n2 = 1;
     while (n2 < total) n2 <<= 1;
     for (int i = tid; i < n2; i += kPlanThreads)
@@ -323,7 +361,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_order_and_packs(
     int32_t *pack_count, int32_t *num_packs, int32_t *mode, const int32_t *rules, int32_t rule_count,
     int32_t force, int32_t hkv, int32_t workers, int32_t buckets, int32_t record_capacity) {
     __shared__ PlanShared sh;
-    stage_order_and_packs(weight, record_count, order, pack_first, pack_count, num_packs, mode, rules,
+    stage_order_and_packs(weight, *record_count, order, pack_first, pack_count, num_packs, mode, rules,
                           rule_count, force, hkv, workers, buckets, record_capacity, sh);
 }
 
@@ -332,52 +370,71 @@ __global__ __launch_bounds__(kPlanThreads) void k_greedy_lists(const int32_t *we
                                                                int32_t *static_next, int32_t hkv,
                                                                int32_t workers) {
     extern __shared__ char dyn[];
-    stage_greedy_lists(weight, record_count, mode, static_head, static_next, hkv, workers,
-                       *reinterpret_cast<GreedyShared *>(dyn));
+    GreedyShared &g = *reinterpret_cast<GreedyShared *>(dyn);
+    stage_greedy_lists(weight, *record_count, *mode, static_head, static_next, hkv, workers, g.keys, g.load,
+                       g.tail);
 }
 
+// Dynamic LDS of the fused kernel.  Region A holds the per-row values between
+// count/scan and record emission, then the LPT loads/tails; region B holds the record
+// weights between emission, ordering and the LPT, where they become the sort keys.
+struct FusedLds {
+    union {
+        struct {
+            int32_t lengths[4096], counts[4096], offsets[4096], chunk[4096];
+        } rows;
+        struct {
+            int32_t load[kGreedyMaxWorkers], tail[kGreedyMaxWorkers];
+        } lpt;
+    } a;
+    union {
+        int32_t weight[kGreedyMaxRecords];
+        uint32_t keys[kGreedyMaxRecords];
+    } b;
+};
+static_assert(sizeof(FusedLds) <= 160 * 1024, "fused plan LDS");
+
+// All stages in one launch; every intermediate that a later stage reads stays in LDS,
+// so the stages wait on no global round trip of their own outputs.
 __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p, int32_t force, int32_t run_greedy,
                                                              int32_t *zero_counters, int32_t num_counters) {
     __shared__ PlanShared sh;
-    extern __shared__ char dyn[];
+    extern __shared__ __align__(16) char dyn[];
+    FusedLds &L = *reinterpret_cast<FusedLds *>(dyn);
     for (int i = threadIdx.x; i < num_counters; i += kPlanThreads) zero_counters[i] = 0;
+    const RowMirror mirror{L.a.rows.lengths, L.a.rows.counts, L.a.rows.offsets, L.a.rows.chunk};
     stage_count_scan(p.lengths, p.splits, p.active, p.counts, p.offsets, p.chunk, p.record_count, p.error,
-                     p.batch_capacity, p.max_splits, p.max_context, sh);
+                     p.batch_capacity, p.max_splits, p.max_context, sh, &mirror);
     if (force == 0) {  // forced R0: counts/offsets only (planning/builder.py:11-14)
         if (threadIdx.x == 0) { *p.mode = 0; *p.num_packs = 0; }
         return;
     }
     __syncthreads();
-    stage_emit_records(p.lengths, p.counts, p.offsets, p.chunk, p.request, p.split, p.begin, p.end, p.weight,
-                       p.batch_capacity, p.max_splits, p.block_kv);
+    const int32_t total = sh.record_count;
+    stage_emit_records(L.a.rows.lengths, L.a.rows.counts, L.a.rows.offsets, L.a.rows.chunk, p.request, p.split,
+                       p.begin, p.end, p.weight, p.batch_capacity, p.max_splits, p.block_kv, L.b.weight);
     __syncthreads();
-    stage_order_and_packs(p.weight, p.record_count, p.order, p.pack_first, p.pack_count, p.num_packs, p.mode,
-                          p.rules, p.rule_count, force, p.kv_heads, p.workers, p.buckets,
-                          p.batch_capacity * p.max_splits, sh);
+    stage_order_and_packs(L.b.weight, total, p.order, p.pack_first, p.pack_count, p.num_packs, p.mode, p.rules,
+                          p.rule_count, force, p.kv_heads, p.workers, p.buckets, p.batch_capacity * p.max_splits,
+                          sh);
     if (run_greedy) {
         __syncthreads();
-        stage_greedy_lists(p.weight, p.record_count, p.mode, p.static_head, p.static_next, p.kv_heads,
-                           p.workers, *reinterpret_cast<GreedyShared *>(dyn));
+        // the LPT's loads and tails take region A (free by now), its keys replace the weights
+        stage_greedy_lists(L.b.weight, total, sh.mode, p.static_head, p.static_next, p.kv_heads, p.workers,
+                           L.b.keys, L.a.lpt.load, L.a.lpt.tail);
     }
 }
 
-size_t greedy_shared_bytes(int32_t record_capacity, int32_t workers) {
-    (void)record_capacity;
-    (void)workers;
-    return sizeof(GreedyShared);
-}
+bool lds_attr_set = false;
 
-bool greedy_attr_set = false;
-
-int prepare_greedy_launch() {
-    if (greedy_attr_set) return 0;
-    const int bytes = (int)sizeof(GreedyShared);
-    if (hipFuncSetAttribute((const void *)k_greedy_lists, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) !=
-            hipSuccess ||
-        hipFuncSetAttribute((const void *)k_build_plan, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) !=
-            hipSuccess)
-        return einval("hipFuncSetAttribute(max dynamic LDS %d) failed", bytes);
-    greedy_attr_set = true;
+int prepare_plan_launch() {
+    if (lds_attr_set) return 0;
+    if (hipFuncSetAttribute((const void *)k_greedy_lists, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)sizeof(GreedyShared)) != hipSuccess ||
+        hipFuncSetAttribute((const void *)k_build_plan, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)sizeof(FusedLds)) != hipSuccess)
+        return einval("hipFuncSetAttribute(max dynamic LDS) failed");
+    lds_attr_set = true;
     return 0;
 }
 
@@ -439,7 +496,7 @@ extern "C" int sgd_greedy_lists(const int32_t *weight, const int32_t *record_cou
     if (record_capacity <= 0 || record_capacity > kGreedyMaxRecords || kv_heads <= 0 || workers <= 0 ||
         workers > kGreedyMaxWorkers)
         return einval("greedy_lists: bad geometry");
-    if (int rc = prepare_greedy_launch()) return rc;
+    if (int rc = prepare_plan_launch()) return rc;
     clear_stale_error();
     hipLaunchKernelGGL(k_greedy_lists, dim3(1), dim3(kPlanThreads), sizeof(GreedyShared), (hipStream_t)stream,
                        weight, record_count, mode, static_head, static_next, kv_heads, workers);
@@ -454,13 +511,9 @@ extern "C" int sgd_build_plan(const sgd_plan_buffers *plan, int32_t force_mode, 
         return rc;
     if (plan->rule_count < 0) return einval("build_plan: negative rule_count");
     if (num_counters < 0 || (num_counters > 0 && !zero_counters)) return einval("build_plan: counters");
-    size_t dyn = 0;
-    if (run_greedy) {
-        if (int rc = prepare_greedy_launch()) return rc;
-        dyn = sizeof(GreedyShared);
-    }
+    if (int rc = prepare_plan_launch()) return rc;
     clear_stale_error();
-    hipLaunchKernelGGL(k_build_plan, dim3(1), dim3(kPlanThreads), dyn, (hipStream_t)stream, *plan, force_mode,
-                       run_greedy, zero_counters, num_counters);
+    hipLaunchKernelGGL(k_build_plan, dim3(1), dim3(kPlanThreads), sizeof(FusedLds), (hipStream_t)stream, *plan,
+                       force_mode, run_greedy, zero_counters, num_counters);
     return launch_status("build_plan");
 }

@@ -102,11 +102,13 @@ def _torch():
     return torch
 
 
-def make_inputs(config, lengths, seed=17, device="cuda", dtype=None, pool_pages=None):
+def make_inputs(config, lengths, seed=17, device="cuda", dtype=None, pool_pages=None,
+                device_pool=False):
     """Paged fixture: (q [Bcap,Hq,D], k/v [pages, page, Hkv, D], table [Bcap, max_pages]).
 
     Pages are a seeded random permutation of a pool of ``pool_pages`` pages (at least the
-    pages the batch needs); unused table entries are -1.  Generated on the CPU.
+    pages the batch needs); unused table entries are -1.  Generated on the CPU, or, with
+    ``device_pool``, the (large) K/V pools are drawn by a seeded generator on ``device``.
     """
     torch = _torch()
     dtype = torch.bfloat16 if dtype is None else dtype
@@ -120,8 +122,13 @@ def make_inputs(config, lengths, seed=17, device="cuda", dtype=None, pool_pages=
         table[row, :count] = perm[cursor:cursor + count].to(torch.int32)
         cursor += count
     shape = (pool, config.page_size, config.kv_heads, config.head_dim)
-    k = torch.randn(shape, generator=g, dtype=torch.float32).to(dtype)
-    v = torch.randn(shape, generator=g, dtype=torch.float32).to(dtype)
+    if device_pool:
+        dg = torch.Generator(device=device).manual_seed(seed + 1)
+        k = torch.randn(shape, generator=dg, device=device, dtype=dtype)
+        v = torch.randn(shape, generator=dg, device=device, dtype=dtype)
+    else:
+        k = torch.randn(shape, generator=g, dtype=torch.float32).to(dtype)
+        v = torch.randn(shape, generator=g, dtype=torch.float32).to(dtype)
     q = torch.randn((config.batch_capacity, config.query_heads, config.head_dim), generator=g,
                     dtype=torch.float32).to(dtype)
     return q.to(device), k.to(device), v.to(device), table.to(device)

@@ -1,20 +1,27 @@
 """Decode-attention benchmark: Llama-3-8B GQA layer, batch 64, on one MI355X.
 
-Workload (the headline configuration): batch 64, 32 q heads / 8 kv heads, head_dim
-128, bf16 KV ~ N(0,1), page_size 1 CSR token indices, contexts
+Workload (the headline configuration, `--workload c2`): batch 64, 32 q heads / 8 kv
+heads, head_dim 128, bf16 KV ~ N(0,1), page_size 1 CSR token indices, contexts
 clip(round(exp(N(ln 1024, 0.8))), 128, 8192) (seeded), a 1M-token KV pool per layer
-with randomly permuted slots.  A step is one hipGraph replay of the plan build
-plus `--layers` layers (counter reset, persistent attention, merge), each layer
-over its own KV pool so the working set exceeds the 256 MB Infinity Cache.
+with randomly permuted slots.  A step is one hipGraph replay of the plan build plus
+`--layers` layers (persistent attention, merge), each layer over its own KV pool so
+the working set exceeds the 256 MB Infinity Cache.  `--workload c3` is the skewed
+batch (2 x 32768 + 126 short requests, up to 64 splits), `--workload c4` the
+Llama-3-70B paged layer (page 16, 64 q / 8 kv, batch 32, contexts in [2048, 16384],
+200k-page pools; `--dtype fp16|bf16`).
 
-Reported per schedule (R1, STATIC, D1, D4, R0): us/layer = replay time / layers,
-achieved GB/s = algorithmic bytes per layer / us/layer.  `value` is the achieved
-HBM GB/s of the fastest schedule.  `roofline` times the attention kernel alone
-(HIP events on the launch stream around each launch, rotating layers) for that
-schedule.  `cpu_baseline` is the FP32 oracle on the same inputs, timed on this
-host (bounded sample stated in the record).
+Reported per schedule (R1, STATIC, STATIC_HOST, D1, D4, R0): us/layer = replay time /
+layers, achieved GB/s = algorithmic bytes per layer / us/layer.  STATIC builds its LPT
+lists on the device inside the replay (the reference's device greedy, a serial
+chain); STATIC_HOST is the reference benchmark's host-static variant
+(benchmarks/bench_decode.py:14-30): C++ heap LPT on the host when the lengths change,
+lists installed after the device R1 plan.  `value` is the achieved HBM GB/s of the
+fastest schedule.  `roofline` times the attention kernel alone (HIP events on the
+launch stream around each launch, rotating layers) for that schedule.
+`cpu_baseline` is the FP32 oracle on the same inputs, timed on this host (bounded
+sample stated in the record).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--workload c2]
 """
 import argparse
 import json
@@ -30,7 +37,15 @@ for _p in (os.path.join(ROOT, "-sglang-decode-_amd"), ROOT):
 
 METRIC = "decode-attn µs/layer + achieved HBM GB/s (% peak), Llama-3-8B GQA shape B=64"
 PEAK_HBM_GBS = 8000.0
-POLICIES = ("R1", "STATIC", "D1", "D4", "R0")
+POLICIES = ("R1", "STATIC", "STATIC_HOST", "D1", "D4", "R0")
+WORKLOADS = {
+    "c2": "llama3-8b decode layer: B=64, 32q/8kv, D=128, bf16, CSR page 1, lognormal(median 1024) "
+          "contexts clipped [128,8192], 1M-token pool per layer",
+    "c3": "skewed decode layer: B=128 (2 x 32768 + 126 x U[32,512]), 32q/8kv, D=128, bf16, CSR page 1, "
+          "splits of up to 512 tokens (max 64), 1M-token pool per layer",
+    "c4": "llama3-70b paged decode layer: B=32, 64q/8kv, D=128, page 16, contexts U[2048,16384], "
+          "200k-page pool per layer",
+}
 
 
 def parse():
@@ -38,7 +53,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--layers", type=int, default=0, help="0 = 4 (c2, c3) or 2 (c4)")
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--dtype", default="bf16", choices=("bf16", "fp16"))
     ap.add_argument("--policies", default=",".join(POLICIES))
     ap.add_argument("--kernel", default="auto")
     ap.add_argument("--workers", type=int, default=0, help="0 = default_workers (2 per CU)")
@@ -87,36 +104,58 @@ def main():
     from sglang_decode.kernels.attention import persistent_decode
     from sglang_decode.runtime.engine import DecodeEngine, PlanKey
     from sglang_decode.runtime.graph import DecodeGraph
+    from sglang_decode.planning.host_static import HostStatic
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
     props = torch.cuda.get_device_properties(dev)
     workers = args.workers or default_workers(dev)
-    base = W.config_for("c2", workers=workers)
-    c = base
-    lengths = W.c2_lengths()
+    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    c = W.config_for(args.workload, workers=workers)
+    lengths = W.lengths_for(args.workload)
     splits = W.split_hints(lengths, c.max_splits)
     batch = len(lengths)
-    pool_tokens = 1 << 20
-    layers = args.layers
+    layers = args.layers or (2 if args.workload == "c4" else 4)
+    csr = c.page_size == 1
     print(f"[bench] device={props.name} CUs={props.multi_processor_count} workers={workers} "
-          f"batch={batch} sumL={sum(lengths)} layers={layers}", flush=True)
+          f"workload={args.workload} batch={batch} sumL={sum(lengths)} layers={layers}", flush=True)
 
-    fx = [W.make_csr_inputs(c, lengths, seed=1000 + i, device=dev, pool_tokens=pool_tokens,
+    if csr:
+        fx = [W.make_csr_inputs(c, lengths, seed=1000 + i, device=dev, pool_tokens=1 << 20, dtype=dtype,
+                                device_pool=True) for i in range(layers)]
+        graph_kw = dict(indptrs=[x[4].numel() for x in fx])
+        tables = [x[4] for x in fx]
+        update_kw = dict(indptrs=[x[3] for x in fx])
+    else:
+        fx = [W.make_inputs(c, lengths, seed=1000 + i, device=dev, dtype=dtype, pool_pages=200_000,
                             device_pool=True) for i in range(layers)]
+        graph_kw = {}
+        tables = [x[3][:batch] for x in fx]
+        update_kw = {}
     bytes_per_layer = W.algorithmic_bytes(lengths, c)
     torch.cuda.synchronize()
 
     results = {}
     engines = {}
+    host_lpt_us = None
     for name in [p for p in args.policies.split(",") if p]:
-        mode = int(Mode[name])
-        engine = DecodeEngine(c, device=dev, layers=layers, force_mode=mode, kernel=args.kernel)
-        key = PlanKey("c2", "hints", (c.query_heads, c.kv_heads, c.head_dim))
-        graph = DecodeGraph(engine, [key] * layers, [(x[1], x[2]) for x in fx],
-                            indptrs=[x[4].numel() for x in fx])
-        graph.update([x[0][:batch] for x in fx], [x[4] for x in fx], lengths, splits,
-                     [x[3] for x in fx])
+        host_static = name == "STATIC_HOST"
+        mode = int(Mode.R1 if host_static else Mode[name])
+        engine = DecodeEngine(c, device=dev, dtype=dtype, layers=layers, force_mode=mode, kernel=args.kernel)
+        if host_static:
+            hs = HostStatic(engine)
+            t0 = time.perf_counter()
+            hs.plan_lists(lengths, splits)
+            host_lpt_us = (time.perf_counter() - t0) * 1e6
+            device_prepare = engine.prepare
+
+            def prepare(device_prepare=device_prepare, hs=hs):
+                device_prepare()
+                hs.apply()
+            engine.prepare = prepare
+        key = PlanKey(args.workload, "hints", (c.query_heads, c.kv_heads, c.head_dim))
+        graph = DecodeGraph(engine, [key] * layers, [(x[1], x[2]) for x in fx], **graph_kw)
+        graph.update([x[0][:batch] for x in fx], tables, lengths, splits, **update_kw)
         graph.capture()
         for _ in range(args.warmup):
             graph.replay()
@@ -143,16 +182,28 @@ def main():
     engine, graph = engines[best]
 
     # correctness of the reported schedule: layer 0 against the FP32 oracle.  The used KV
-    # rows are gathered to the host first (outside any timed region).
+    # rows / pages are gathered to the host first (outside any timed region).
     from oracle import attention as OA
     x = fx[0]
-    idx = x[4].long()
-    host = (x[0].cpu(), x[1][idx].cpu(), x[2][idx].cpu(), x[3].cpu(),
-            torch.arange(idx.numel(), dtype=torch.int32))
+    if csr:
+        idx = x[4].long()
+        host = (x[0].cpu(), x[1][idx].cpu(), x[2][idx].cpu(), x[3].cpu(),
+                torch.arange(idx.numel(), dtype=torch.int32))
+        oracle = lambda: OA.csr_attention(*host, lengths)[:batch]
+    else:
+        used = [x[3][r, :(n + c.page_size - 1) // c.page_size].long() for r, n in enumerate(lengths)]
+        flat = torch.cat(used)
+        table = torch.full((batch, c.max_pages), -1, dtype=torch.int32)
+        cursor = 0
+        for r, u in enumerate(used):
+            table[r, :u.numel()] = torch.arange(cursor, cursor + u.numel(), dtype=torch.int32)
+            cursor += u.numel()
+        host = (x[0][:batch].cpu(), x[1][flat].cpu(), x[2][flat].cpu(), table)
+        oracle = lambda: OA.paged_attention(*host, lengths, c.page_size)[:batch]
     check, cpu_times, expected = None, [], None
     if not (args.no_check and args.no_cpu_baseline):
         t0 = time.perf_counter()
-        expected = OA.csr_attention(*host, lengths)[:batch]
+        expected = oracle()
         cpu_times.append(time.perf_counter() - t0)
     if not args.no_check:
         graph.replay()
@@ -178,10 +229,14 @@ def main():
         x = fx[li]
         layer.counter.zero_()
         ev[i][0].record(stream)
+        if csr:
+            ks = (x[1].stride(0), 0, x[1].stride(1), x[1].stride(2))
+            vs = (x[2].stride(0), 0, x[2].stride(1), x[2].stride(2))
+            pts = (0, 0)
+        else:
+            ks, vs, pts = x[1].stride(), x[2].stride(), graph.pages[li].stride()
         persistent_decode(p, layer, graph.q[li], x[1], x[2], graph.pages[li], graph.indptr[li],
-                          c.head_dim ** -0.5, (x[1].stride(0), 0, x[1].stride(1), x[1].stride(2)),
-                          (x[2].stride(0), 0, x[2].stride(1), x[2].stride(2)), (0, 0), True,
-                          args.kernel)
+                          c.head_dim ** -0.5, ks, vs, pts, csr, args.kernel)
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     durs = [a.elapsed_time(b) * 1000.0 for a, b in ev[len(ev) // 10:]]
@@ -211,7 +266,7 @@ def main():
         # the sample: the full layer (all requests) on host-resident fp32-upcast inputs
         for _ in range(2):
             t0 = time.perf_counter()
-            OA.csr_attention(*host, lengths)
+            oracle()
             cpu_times.append(time.perf_counter() - t0)
         t = statistics.median(cpu_times)
         cpu = dict(value=round(t * 1e6, 1), unit="us/layer", cores=1, kind="port",
@@ -224,10 +279,9 @@ def main():
     line = {
         "metric": METRIC, "value": round(r["gbps"], 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(r["ms_per_step"], 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (seeded lognormal contexts, N(0,1) bf16 q/K/V, permuted 1M-token pools)",
-        "config": {"workload": "llama3-8b decode layer: B=64, 32q/8kv, D=128, bf16, CSR page 1, "
-                               "lognormal(median 1024) contexts clipped [128,8192], 1M-token pool",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": args.dtype,
+        "data": f"synthetic (seeded contexts, N(0,1) {args.dtype} q/K/V, randomly permuted KV pools)",
+        "config": {"workload": WORKLOADS[args.workload], "name": args.workload,
                    "batch": batch, "sum_context": sum(lengths), "layers_per_step": layers,
                    "schedule": best, "workers": workers, "kernel": args.kernel,
                    "splits_total": sum(splits)},
@@ -236,6 +290,7 @@ def main():
         "tokens_per_s": round(batch / (r["us_per_layer"] * 1e-6), 1),
         "kv_tokens_per_s": round(sum(lengths) / (r["us_per_layer"] * 1e-6), 1),
         "schedules": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in results.items()},
+        "host_lpt_us": None if host_lpt_us is None else round(host_lpt_us, 1),
         "check": check,
         "roofline": roofline,
         "cpu_baseline": cpu,

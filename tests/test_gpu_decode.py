@@ -174,10 +174,11 @@ def test_stream_short_tasks_and_small_worker_counts(mode):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mode", list(Mode))
-@pytest.mark.parametrize("hq", [64, 128])
-def test_mfma_kernel_groups_8_and_16_paged(hq, mode, dtype):
-    """Group 8 (Llama-3-70B heads) and 16 on the MFMA kernel: page 16, ragged lengths
-    (a 1-token request, a 31-token one that ends mid-tile, an empty row)."""
+@pytest.mark.parametrize("hq", [8, 32, 64, 128])
+def test_mfma_kernel_groups_paged(hq, mode, dtype):
+    """Groups 1, 4, 8 (Llama-3-70B heads) and 16 on the MFMA kernel (heads padded to 16):
+    page 16, ragged lengths (a 1-token request, a 31-token one that ends mid-tile, an
+    empty row)."""
     c = DecodeConfig(batch_capacity=6, max_splits=16, max_context=4096, query_heads=hq, kv_heads=8,
                      head_dim=128, page_size=16, workers=64)
     lengths = [4096, 1, 999, 31, 0, 2500]

@@ -224,3 +224,26 @@ def test_engine_validates_before_launch():
     assert engine.layers[0].partial.shape == (4, 8, 16, 128)
     assert engine.layers[0].lse.shape == (4, 8, 16)
     assert Mode.D4 == 4
+
+
+def test_host_static_schedule_installs_reference_lists(plan_vectors):
+    """HostStatic (the benchmark's host-planned STATIC schedule) puts the reference's LPT
+    lists into the plan and forces mode 2, with device ops only (here on a CPU plan)."""
+    import torch
+    from sglang_decode.planning.host_static import HostStatic
+    from sglang_decode.runtime.engine import DecodeEngine
+    case = next(c for c in plan_vectors if c["name"].startswith("B/"))
+    cc = case["config"]
+    c = DecodeConfig(batch_capacity=cc["batch_capacity"], max_splits=cc["max_splits"],
+                     max_context=cc["max_context"], kv_heads=cc["kv_heads"],
+                     query_heads=4 * cc["kv_heads"], workers=cc["workers"])
+    engine = DecodeEngine(c, device="cpu", layers=1)
+    hs = HostStatic(engine)
+    hs.plan_lists(case["lengths"], case["splits"])
+    hs.apply()
+    heads, nxt = R.lists_to_links(case["static_lists"], c.workers, c.task_capacity)
+    assert engine.plan.static_head.tolist() == heads
+    assert engine.plan.static_next.tolist() == nxt
+    assert engine.plan.mode.item() == 2
+    with pytest.raises(ValueError):  # capacities are checked on the host
+        hs.plan_lists([c.max_context + 1], [1])
