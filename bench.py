@@ -8,7 +8,8 @@ with randomly permuted slots.  A step is one hipGraph replay of the plan build p
 the working set exceeds the 256 MB Infinity Cache.  `--workload c3` is the skewed
 batch (2 x 32768 + 126 short requests, up to 64 splits), `--workload c4` the
 Llama-3-70B paged layer (page 16, 64 q / 8 kv, batch 32, contexts in [2048, 16384],
-200k-page pools; `--dtype fp16|bf16`).
+200k-page pools; `--dtype fp16|bf16`), `--workload c5` the 32-layer step of the
+8B shape at batch 64 (contexts lognormal, median 2048).
 
 Reported per schedule (R1, STATIC, STATIC_HOST, D1, D4, R0): us/layer = replay time /
 layers, achieved GB/s = algorithmic bytes per layer / us/layer.  STATIC builds its LPT
@@ -45,6 +46,8 @@ WORKLOADS = {
           "splits of up to 512 tokens (max 64), 1M-token pool per layer",
     "c4": "llama3-70b paged decode layer: B=32, 64q/8kv, D=128, page 16, contexts U[2048,16384], "
           "200k-page pool per layer",
+    "c5": "llama3-8b 32-layer decode step: B=64, 32q/8kv, D=128, bf16, CSR page 1, lognormal(median "
+          "2048) contexts clipped [128,16384], 256k-token pool per layer",
 }
 
 
@@ -115,13 +118,14 @@ def main():
     lengths = W.lengths_for(args.workload)
     splits = W.split_hints(lengths, c.max_splits)
     batch = len(lengths)
-    layers = args.layers or (2 if args.workload == "c4" else 4)
+    layers = args.layers or {"c4": 2, "c5": 32}.get(args.workload, 4)
     csr = c.page_size == 1
     print(f"[bench] device={props.name} CUs={props.multi_processor_count} workers={workers} "
           f"workload={args.workload} batch={batch} sumL={sum(lengths)} layers={layers}", flush=True)
 
     if csr:
-        fx = [W.make_csr_inputs(c, lengths, seed=1000 + i, device=dev, pool_tokens=1 << 20, dtype=dtype,
+        pool_tokens = 1 << (18 if args.workload == "c5" else 20)
+        fx = [W.make_csr_inputs(c, lengths, seed=1000 + i, device=dev, pool_tokens=pool_tokens, dtype=dtype,
                                 device_pool=True) for i in range(layers)]
         graph_kw = dict(indptrs=[x[4].numel() for x in fx])
         tables = [x[4] for x in fx]

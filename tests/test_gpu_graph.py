@@ -94,3 +94,65 @@ def test_csr_graph_replay_shrinking_batches(mode):
         for i, x in enumerate(fx):
             exp = OA.csr_attention(x[0], x[1], x[2], indptrs[i], indices[i], lengths)
             close(outs[i][:batch], exp[:batch])
+
+
+def _csr_step(fx, lengths):
+    """Per-layer kv_indptr / kv_indices of one step: the first L tokens of each request's
+    slots in that layer's pool."""
+    indptrs, indices = [], []
+    for x in fx:
+        full_ptr = x[3].cpu().tolist()
+        idx = x[4]
+        parts = [idx[full_ptr[r]:full_ptr[r] + lengths[r]] for r in range(len(lengths))]
+        ptr = torch.zeros(len(lengths) + 1, dtype=torch.int32)
+        ptr[1:] = torch.cumsum(torch.tensor(lengths), 0)
+        indptrs.append(ptr.cuda())
+        indices.append(torch.cat(parts))
+    return indptrs, indices
+
+
+def _oracle_layer(x, indptr, indices, lengths):
+    """FP32 oracle on the rows the step uses, gathered on the device first."""
+    rows = indices.long()
+    k, v = x[1][rows].cpu(), x[2][rows].cpu()
+    local = torch.arange(rows.numel(), dtype=torch.int32)
+    return OA.csr_attention(x[0][:len(lengths)].cpu(), k, v, indptr.cpu(), local, lengths)
+
+
+def test_llama8b_32_layer_graph_shrinking_batches():
+    """The 32-layer decode step under one hipGraph: 8B heads, batch 64 -> 48 -> 17 -> 1
+    with contexts growing by one per step from a lognormal start (median 2048), the plan
+    rebuilt on the device at every replay (a D4 rule for non-uniform batches; the uniform
+    batch-1 step takes the device bypass to R1), per-layer counters and scratch; the host
+    rejects an over-capacity step before touching the graph."""
+    c = W.config_for("c5")
+    base = W.c5_lengths()
+    layers = 32
+    rules = [PolicyRule(1, c.task_capacity, 101, 10000, int(Mode.D4))]
+    steps = len(W.C5_BATCHES)
+    pool = sum(base) + 64 * steps
+    fx = [W.make_csr_inputs(c, [x + steps for x in base], seed=500 + i, pool_tokens=pool, device_pool=True)
+          for i in range(layers)]
+    engine = DecodeEngine(c, layers=layers, rules=rules)
+    key = PlanKey("c5", "hints", (c.query_heads, c.kv_heads, c.head_dim))
+    graph = DecodeGraph(engine, [key] * layers, [(x[1], x[2]) for x in fx],
+                        indptrs=[x[4].numel() for x in fx])
+    checked = (0, 17, 31)
+    for step, batch in enumerate(W.C5_BATCHES):
+        lengths = [x + step for x in base[:batch]]
+        indptrs, indices = _csr_step(fx, lengths)
+        graph.update([x[0][:batch] for x in fx], indices, lengths, W.split_hints(lengths, c.max_splits),
+                     indptrs)
+        if step == 0:
+            graph.capture()
+        for layer in engine.layers:
+            layer.partial.fill_(float("nan"))
+        outs = graph.replay()
+        torch.cuda.synchronize()
+        assert engine.plan.mode.item() == (Mode.R1 if batch == 1 else Mode.D4)
+        for i in checked:
+            close(outs[i][:batch], _oracle_layer(fx[i], indptrs[i], indices[i], lengths)[:batch])
+    # over capacity: the host refuses before the graph is touched
+    with pytest.raises(ValueError):
+        graph.update([x[0][:1] for x in fx], [x[4][:1] for x in fx], [c.max_context + 1], [1],
+                     [torch.tensor([0, 1], dtype=torch.int32, device="cuda")] * layers)
