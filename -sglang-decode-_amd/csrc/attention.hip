@@ -61,6 +61,9 @@ int check_args(const sgd_decode_args *args) {
     if (a.csr && (a.page_size != 1 || !a.indptr)) return einval("persistent_decode: CSR needs page_size 1 + indptr");
     if (!a.q || !a.k || !a.v || !a.pages || !a.partial || !a.lse || !a.counter)
         return einval("persistent_decode: null buffer");
+    if (a.dispatch0 && a.dispatch_workers != a.workers)
+        return einval("persistent_decode: dispatch0 holds %d workers' first tasks, the launch has %d",
+                      a.dispatch_workers, a.workers);
     return 0;
 }
 
@@ -69,10 +72,13 @@ int resolve_kernel(const sgd_decode_args &a) {
     switch (a.kernel) {
         case SGD_KERNEL_AUTO:
             // The stream kernel is one 1024-thread workgroup per CU: with more workers
-            // than CUs they would run in turns, so the two-per-CU kernel takes over.
+            // than CUs they would run in turns, so a two-per-CU kernel takes over --
+            // the MFMA one (also for groups <= 4, heads padded: at the Llama-3-8B
+            // layer it measured 3-4 us faster than the VALU per-task kernel), else the
+            // VALU one, else the generic kernel.
             if (stream_supported(a) && a.workers <= device_cus()) return SGD_KERNEL_STREAM;
-            if (valu_supported(a)) return SGD_KERNEL_VALU;
             if (mfma_supported(a)) return SGD_KERNEL_MFMA;
+            if (valu_supported(a)) return SGD_KERNEL_VALU;
             return SGD_KERNEL_GENERIC;
         case SGD_KERNEL_GENERIC:
             return SGD_KERNEL_GENERIC;

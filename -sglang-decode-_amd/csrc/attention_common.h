@@ -52,41 +52,82 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Runs `run(task, mode)` for every task of this worker.  All threads of the
-// workgroup execute it uniformly; `sh_cursor` is one int of LDS.
+// This worker's first task as resolved by the plan (sgd_plan_buffers.dispatch0), when
+// the launch may use it: modes R1, D1, D4, and a table built for this mode and worker
+// count (entry 0's tag).  The host guarantees dispatch0 has an entry per worker.
+struct FirstTask {
+    bool valid;
+    int32_t task, count;
+    TaskInfo info;
+};
+
+__device__ __forceinline__ FirstTask first_task(const sgd_decode_args &a, int32_t mode) {
+    FirstTask f;
+    f.valid = false;
+    if (!a.dispatch0) return f;
+    const int32_t *e = a.dispatch0 + 8 * blockIdx.x;  // loaded with the tag, in one round trip
+    const int32_t tag = a.dispatch0[7];
+    f.task = e[0];
+    f.count = e[1];
+    f.info.request = e[2];
+    f.info.split = e[3];
+    f.info.start = e[4];
+    f.info.end = e[5];
+    f.info.group = e[6];
+    f.valid = (mode == 1 || mode == 3 || mode == 4) && tag == mode + 8 * a.workers;
+    return f;
+}
+
+// Runs `run(task, mode, pre)` for every task of this worker, where pre is the task's
+// resolved TaskInfo when the plan supplied it (the first task; null otherwise).  All
+// threads of the workgroup execute it uniformly; `sh_cursor` is one int of LDS.  With
+// a first-task table in D1/D4, worker w runs pack w first and its claims are
+// workers + (counter): every pack still runs exactly once.
 template <class Run>
 __device__ void for_each_task(const sgd_decode_args &a, int32_t *sh_cursor, Run &&run) {
     const int32_t worker = blockIdx.x;
     const int32_t mode = *a.mode;
+    const FirstTask first = first_task(a, mode);
     const int32_t total = *a.record_count * a.kv_heads;
     const bool dynamic = mode >= 3;
+    const int32_t claim_base = (dynamic && first.valid) ? a.workers : 0;
+    auto claim = [&]() {
+        if (threadIdx.x == 0)
+            *sh_cursor = claim_base + __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const int32_t c = *sh_cursor;
+        __syncthreads();  // every thread has read the claim before the next one overwrites it
+        return c;
+    };
     int32_t cursor, limit;
     if (dynamic) {
-        if (threadIdx.x == 0) *sh_cursor = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED,
-                                                                  __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        cursor = *sh_cursor;
         limit = *a.num_packs;
+        if (first.valid) {
+            if (first.task >= 0) {
+                for (int32_t i = 0; i < first.count; ++i) run(first.task + i, mode, i == 0 ? &first.info : nullptr);
+            }
+        }
+        cursor = claim();
     } else if (mode == 2) {
         cursor = a.static_head[worker];
         limit = total;
     } else {
         cursor = worker;
         limit = total;
+        if (first.valid && cursor < limit) {  // R1: task `worker`, already resolved
+            run(cursor, mode, &first.info);
+            cursor += a.workers;
+        }
     }
     while (cursor >= 0 && cursor < limit) {
-        int32_t first = cursor, count = 1;
+        int32_t first_t = cursor, count = 1;
         if (dynamic) {
-            first = a.pack_first[cursor];
+            first_t = a.pack_first[cursor];
             count = a.pack_count[cursor];
         }
-        for (int32_t i = 0; i < count; ++i) run(first + i, mode);
+        for (int32_t i = 0; i < count; ++i) run(first_t + i, mode, (const TaskInfo *)nullptr);
         if (dynamic) {
-            __syncthreads();
-            if (threadIdx.x == 0) *sh_cursor = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED,
-                                                                      __HIP_MEMORY_SCOPE_AGENT);
-            __syncthreads();
-            cursor = *sh_cursor;
+            cursor = claim();
         } else if (mode == 2) {
             cursor = a.static_next[cursor];
         } else {

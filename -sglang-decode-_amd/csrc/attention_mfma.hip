@@ -184,8 +184,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
     const int32_t G = a.query_heads / a.kv_heads;
     const float scale2 = a.scale * kLog2e;
 
-    for_each_task(a, &sh.cursor, [&](int32_t task, int32_t mode) {
-        const TaskInfo ti = decode_task(a, task, mode);
+    for_each_task(a, &sh.cursor, [&](int32_t task, int32_t mode, const TaskInfo *pre) {
+        const TaskInfo ti = pre ? *pre : decode_task(a, task, mode);
         Src t;
         t.request = uni(ti.request);
         t.start = uni(ti.start);

@@ -352,6 +352,12 @@ __device__ void schedule(StreamShared &sh, const sgd_decode_args &a, int lane) {
     const bool dynamic = mode >= 3;
     const int32_t num_packs = dynamic ? uni(*a.num_packs) : 0;
     const int32_t active = mode == 0 ? uni(*a.active) : 0;
+    // The plan may have resolved this worker's first task (R1, D1/D4): it is published
+    // without the order -> record walk, and in D1/D4 pack `worker` is taken without a
+    // claim; later claims are then W + counter (every pack still runs once).
+    const FirstTask first = first_task(a, mode);
+    bool first_pending = first.valid;
+    const int32_t claim_base = (dynamic && first.valid) ? W : 0;
     int32_t seq = 0, base = 0;
     int64_t rr = 0;                          // R0/R1: tasks enumerated so far
     int32_t chain = -1;                      // STATIC: last task taken from the list
@@ -359,7 +365,14 @@ __device__ void schedule(StreamShared &sh, const sgd_decode_args &a, int lane) {
     for (;;) {
         // 1. enumerate up to 64 tasks, one per lane
         int32_t t = -1, nb = 0;
-        if (mode <= 1) {
+        bool pre0 = false;  // lane 0's task is the plan-resolved first task
+        if (mode == 1 && first_pending) {
+            first_pending = false;
+            pre0 = first.task >= 0;
+            nb = pre0 ? 1 : 0;
+            t = pre0 && lane == 0 ? first.task : -1;
+            rr = 1;
+        } else if (mode <= 1) {
             const int64_t tt = (int64_t)blockIdx.x + (rr + lane) * W;
             t = tt < total ? (int32_t)tt : -1;
             const int64_t left = total > (int64_t)blockIdx.x + rr * W
@@ -374,12 +387,19 @@ __device__ void schedule(StreamShared &sh, const sgd_decode_args &a, int lane) {
                 nb = 1;
             }
         } else {
-            if (pack_left == 0) {
+            if (first_pending) {
+                first_pending = false;
+                if (first.task >= 0) {
+                    pack_next = first.task;
+                    pack_left = first.count;
+                    pre0 = true;
+                }
+            } else if (pack_left == 0) {
                 // claim only when fewer than kQueueTiles published tiles are unreserved
                 while (base - lds_acquire(&sh.next_tile) >= kQueueTiles) __builtin_amdgcn_s_sleep(2);
                 int32_t c = 0;
                 if (lane == 0) c = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                c = uni(c);
+                c = claim_base + uni(c);
                 if (c >= 0 && c < num_packs) {
                     pack_next = uni(a.pack_first[c]);
                     pack_left = max(uni(a.pack_count[c]), 0);
@@ -394,7 +414,14 @@ __device__ void schedule(StreamShared &sh, const sgd_decode_args &a, int lane) {
 
         // 2. resolve each lane's task (kernels/attention.py:23-47)
         int32_t request = 0, split = 0, start = 0, end = 0, group = 0, ind0 = 0;
-        if (lane < nb && t >= 0) {
+        if (pre0 && lane == 0) {
+            request = first.info.request;
+            split = first.info.split;
+            start = first.info.start;
+            end = first.info.end;
+            group = first.info.group;
+            if constexpr (CSR) ind0 = a.indptr[request];
+        } else if (lane < nb && t >= 0) {
             group = t % hkv;
             int32_t rec = t / hkv;
             if (mode == 0) {

@@ -56,8 +56,8 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
     const int page_shift = __builtin_ctz((unsigned)a.page_size);  // page_size is a power of two here
     const int32_t page_mask = a.page_size - 1;
 
-    for_each_task(a, &sh.cursor, [&](int32_t task, int32_t mode) {
-        const TaskInfo ti = decode_task(a, task, mode);
+    for_each_task(a, &sh.cursor, [&](int32_t task, int32_t mode, const TaskInfo *pre) {
+        const TaskInfo ti = pre ? *pre : decode_task(a, task, mode);
         __syncthreads();  // the previous task's merge is done with shared memory
         if (wave == 0) {  // stage the group's q rows; heads >= G are zero
             const int h = lane >> 4, c = lane & 15;

@@ -35,6 +35,7 @@ struct PlanShared {
     int32_t bucket_packed_tasks[kMaxBuckets];
     int32_t mode;
     int32_t record_count;
+    int32_t num_packs;
     int32_t max_w, min_w;
     int32_t red_max[16], red_min[16];
 };
@@ -142,7 +143,8 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
                                       int32_t *pack_first, int32_t *pack_count, int32_t *num_packs,
                                       int32_t *mode_out, const int32_t *rules, int32_t rule_count,
                                       int32_t force, int32_t hkv, int32_t workers, int32_t buckets,
-                                      int32_t record_capacity, PlanShared &sh) {
+                                      int32_t record_capacity, PlanShared &sh,
+                                      int32_t *order_mirror = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int per = (record_capacity + kPlanThreads - 1) / kPlanThreads;
     const int i0 = tid * per;
@@ -182,7 +184,10 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
     const int32_t mode = sh.mode, max_w = sh.max_w;
     if (mode == 0 || mode == 1) {
         for (int i = tid; i < total; i += kPlanThreads) order[i] = i;
-        if (tid == 0) *num_packs = 0;
+        if (tid == 0) {
+            *num_packs = 0;
+            sh.num_packs = 0;
+        }
         return;
     }
     // Stable partition by bucket, heaviest first.  Each thread owns a contiguous
@@ -223,6 +228,7 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
             pack_base += count;
         }
         *num_packs = pack_base;
+        sh.num_packs = pack_base;
     }
     __syncthreads();
     int32_t rank[kMaxBuckets];
@@ -237,6 +243,7 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
         for (int q = 0; q < kMaxBuckets; ++q)
             if (q == b) { r = rank[q]; rank[q] = r + 1; }
         order[sh.bucket_record_base[b] + r] = i;
+        if (order_mirror) order_mirror[sh.bucket_record_base[b] + r] = i;
     }
     for (int b = buckets - 1; b >= 0; --b) {
         const int32_t count = sh.bucket_pack_count[b], width = sh.bucket_width[b];
@@ -336,6 +343,49 @@ __device__ void stage_greedy_lists(const int32_t *weight, int32_t total, int32_t
     }
 }
 
+// ---------------------------------------------------------------- first tasks
+// Each worker's first task for the attention launch (R1: task w; D1/D4: the first task
+// of pack w, which the launch then assigns to worker w instead of claiming it), with
+// its record resolved: {task, tasks in the pack, request, split, begin, end, group,
+// mode + 8 * workers}.  Pack w is located from the bucket tables in sh exactly as
+// stage_order_and_packs lays the packs out; order comes from its LDS mirror.  The record
+// fields are re-read from global memory (written by this workgroup before a barrier).
+__device__ void stage_dispatch0(int32_t *out, const int32_t *order_mirror, const int32_t *request,
+                                const int32_t *split, const int32_t *begin, const int32_t *end, int32_t total,
+                                int32_t hkv, int32_t workers, int32_t buckets, const PlanShared &sh) {
+    const int32_t mode = sh.mode;
+    for (int w = threadIdx.x; w < workers; w += kPlanThreads) {
+        int32_t task = -1, count = 0, rec = -1;
+        if (mode == 1) {
+            if (w < total * hkv) {
+                task = w;
+                count = 1;
+                rec = w / hkv;  // mode 1 writes the identity order
+            }
+        } else if ((mode == 3 || mode == 4) && w < sh.num_packs) {
+            for (int b = buckets - 1; b >= 0; --b) {
+                const int32_t p = w - sh.bucket_pack_base[b];
+                if (p < 0 || p >= sh.bucket_pack_count[b]) continue;
+                const int32_t width = sh.bucket_width[b], pp = sh.bucket_packed_packs[b];
+                const bool packed = p < pp;
+                task = sh.bucket_record_base[b] * hkv + (packed ? p * width : sh.bucket_packed_tasks[b] + p - pp);
+                count = packed ? width : 1;
+                rec = order_mirror[task / hkv];
+                break;
+            }
+        }
+        int32_t *e = out + 8 * w;
+        e[0] = task;
+        e[1] = count;
+        e[2] = rec >= 0 ? request[rec] : 0;
+        e[3] = rec >= 0 ? split[rec] : 0;
+        e[4] = rec >= 0 ? begin[rec] : 0;
+        e[5] = rec >= 0 ? end[rec] : 0;
+        e[6] = task >= 0 ? task % hkv : 0;
+        e[7] = mode + 8 * workers;
+    }
+}
+
 // ---------------------------------------------------------------- kernels
 __global__ __launch_bounds__(kPlanThreads) void k_count_scan(const int32_t *lengths, const int32_t *splits,
                                                              const int32_t *active, int32_t *counts,
@@ -376,13 +426,15 @@ __global__ __launch_bounds__(kPlanThreads) void k_greedy_lists(const int32_t *we
 }
 
 // Dynamic LDS of the fused kernel.  Region A holds the per-row values between
-// count/scan and record emission, then the LPT loads/tails; region B holds the record
-// weights between emission, ordering and the LPT, where they become the sort keys.
+// count/scan and record emission, then the order (for the first-task stage), then the
+// LPT loads/tails; region B holds the record weights between emission, ordering and the
+// LPT, where they become the sort keys.
 struct FusedLds {
     union {
         struct {
             int32_t lengths[4096], counts[4096], offsets[4096], chunk[4096];
         } rows;
+        int32_t order[kGreedyMaxRecords];
         struct {
             int32_t load[kGreedyMaxWorkers], tail[kGreedyMaxWorkers];
         } lpt;
@@ -414,9 +466,16 @@ __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p,
     stage_emit_records(L.a.rows.lengths, L.a.rows.counts, L.a.rows.offsets, L.a.rows.chunk, p.request, p.split,
                        p.begin, p.end, p.weight, p.batch_capacity, p.max_splits, p.block_kv, L.b.weight);
     __syncthreads();
+    // region A (the row values) is free after emission: it takes the order mirror
+    int32_t *order_mirror = L.a.order;
     stage_order_and_packs(L.b.weight, total, p.order, p.pack_first, p.pack_count, p.num_packs, p.mode, p.rules,
                           p.rule_count, force, p.kv_heads, p.workers, p.buckets, p.batch_capacity * p.max_splits,
-                          sh);
+                          sh, order_mirror);
+    if (p.dispatch0) {
+        __syncthreads();
+        stage_dispatch0(p.dispatch0, order_mirror, p.request, p.split, p.begin, p.end, total, p.kv_heads,
+                        p.workers, p.buckets, sh);
+    }
     if (run_greedy) {
         __syncthreads();
         // the LPT's loads and tails take region A (free by now), its keys replace the weights

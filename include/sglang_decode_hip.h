@@ -102,11 +102,20 @@ typedef struct sgd_plan_buffers {
     int32_t *record_count, *num_packs, *mode, *error; /* [1] each */
     int32_t *static_head, *static_next;               /* [workers], [T] */
     const int32_t *rules;                             /* [max(rule_count,1)][5] */
+    int32_t *dispatch0;                               /* optional [workers][8], see below; may be NULL */
     int32_t rule_count;
     int32_t batch_capacity, max_splits, max_context, kv_heads, workers, block_kv, buckets;
 } sgd_plan_buffers;
 
 /*
+ * dispatch0 (no reference counterpart): each worker's first task, resolved by the
+ * plan so that an attention launch need not walk order -> record (and, in D1/D4,
+ * claim -> pack) before its first loads.  Entry w = {task, tasks in the first pack,
+ * request, split, begin, end, kv group, mode + 8 * workers}; task = -1 when the worker
+ * has none.  Written by sgd_build_plan for modes R1, D1 and D4 only.  When a launch
+ * uses it in D1/D4, worker w runs pack w first and its later claims are
+ * workers + (claim counter) -- every pack is still run exactly once.
+ *
  * Whole plan build in one launch (count/scan, records, order and packs, and,
  * when run_greedy != 0, the STATIC lists).  Same results as the four stage
  * entries above in the order of planning/builder.py:6-28, including the forced
@@ -131,12 +140,14 @@ typedef struct sgd_decode_args {
     const int32_t *static_head, *static_next;
     float *partial;                 /* [bcap, Hq, smax, D] */
     float *lse;                     /* [bcap, Hq, smax] */
+    const int32_t *dispatch0;       /* optional: sgd_build_plan's dispatch0 of this plan (same workers), or NULL */
     float scale;
     int32_t _pad0;
     int64_t q_stride[3], k_stride[4], v_stride[4], pt_stride[2];
     int32_t query_heads, kv_heads, head_dim, max_splits, page_size, csr, dtype, workers;
     int32_t kernel;                 /* enum sgd_kernel */
-    int32_t _pad1;
+    int32_t dispatch_workers;       /* entries in dispatch0 (its plan's workers); must equal workers
+                                       when dispatch0 is set */
 } sgd_decode_args;
 
 /*

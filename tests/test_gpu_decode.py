@@ -38,7 +38,7 @@ def run(engine, lengths, inputs, indptr=None, splits=None, scale=None):
     return out
 
 
-@pytest.mark.parametrize("kernel", ["auto", "generic", "valu", "stream"])
+@pytest.mark.parametrize("kernel", ["auto", "generic", "valu", "stream", "mfma"])
 @pytest.mark.parametrize("mode", list(Mode))
 @pytest.mark.parametrize("lengths", [[0, 1, 17, 33, 257, 513], [256] * 24 + [1536] * 4 + [16384] * 4])
 def test_outputs_and_plan_every_mode(mode, lengths, kernel):
@@ -85,7 +85,7 @@ def test_csr_small_config(mode):
     close(out[:len(lengths)], OA.csr_attention(q, k, v, indptr, indices, lengths)[:len(lengths)])
 
 
-@pytest.mark.parametrize("kernel", ["valu", "stream"])
+@pytest.mark.parametrize("kernel", ["valu", "stream", "mfma"])
 @pytest.mark.parametrize("mode", [Mode.R1, Mode.STATIC, Mode.D1, Mode.D4, Mode.R0])
 def test_csr_llama8b_shape(mode, kernel):
     c = W.config_for("c2")
@@ -139,7 +139,7 @@ def test_invalid_metadata_writes_nan_and_schedules_nothing():
     assert torch.isnan(out.float()).all()
 
 
-@pytest.mark.parametrize("kernel", ["valu", "stream"])
+@pytest.mark.parametrize("kernel", ["valu", "mfma", "stream"])
 def test_reused_output_buffer_and_repeated_execute(kernel):
     c = W.config_for("c1")
     lengths = [200, 16, 100, 50]
@@ -149,7 +149,7 @@ def test_reused_output_buffer_and_repeated_execute(kernel):
     out2 = engine.execute(q, k, v, indices, indptr=indptr)  # same plan, second execute
     torch.cuda.synchronize()
     assert out2.data_ptr() == engine.layers[0].output.data_ptr()
-    if kernel == "valu":
+    if kernel in ("valu", "mfma"):
         assert torch.equal(out1, out2)  # fixed merge order: bitwise repeatable
     else:
         # the stream kernel merges the waves' softmax states in arrival order, so a

@@ -121,3 +121,46 @@ def test_fused_plan_clears_counters():
     counters = torch.full((5,), 1234, dtype=torch.int32, device="cuda")
     build_plan(plan, -1, counters=counters)
     assert counters.tolist() == [0] * 5
+
+
+def expected_dispatch0(ref, c, mode):
+    """Each worker's first task from the oracle plan: R1 task w, D1/D4 the first task
+    of pack w, with its record fields."""
+    hkv, workers = c.kv_heads, c.workers
+    total = ref["record_count"] * hkv
+    rows = []
+    for w in range(workers):
+        task, count = -1, 0
+        if mode == 1 and w < total:
+            task, count = w, 1
+        elif mode in (3, 4) and w < ref["num_packs"]:
+            task, count = ref["pack_first"][w], ref["pack_count"][w]
+        if task >= 0:
+            rec = ref["order"][task // hkv]
+            fields = [ref[k][rec] for k in ("request", "split", "begin", "end")]
+        else:
+            fields = [0, 0, 0, 0]
+        rows.append([task, count] + fields + [task % hkv if task >= 0 else 0, mode + 8 * workers])
+    return rows
+
+
+@pytest.mark.parametrize("force", [1, 3, 4])
+def test_first_task_table_matches_oracle(force):
+    """sgd_build_plan's dispatch0: each worker's first task, resolved exactly as the
+    attention dispatch would resolve it (task -> order -> record)."""
+    for name in ("c1", "c2", "c3", "c5"):
+        for workers in (7, 256):
+            c = W.config_for(name, workers=workers)
+            lengths = W.lengths_for(name)
+            splits = W.split_hints(lengths, c.max_splits)
+            plan = PlanBuffers(c, "cuda")
+            load(plan, lengths, splits)
+            plan.dispatch0.fill_(-9)
+            build_plan(plan, force)
+            assert plan.dispatch_valid
+            lw = list(lengths) + [0] * (c.batch_capacity - len(lengths))
+            sw = list(splits) + [1] * (c.batch_capacity - len(splits))
+            ref = OP.full_plan(lw, sw, len(lengths), cfg_ns(c), [], force)
+            assert plan.dispatch0.cpu().tolist() == expected_dispatch0(ref, c, force), (name, workers)
+    build_plan(plan, force, fused=False)
+    assert not plan.dispatch_valid  # the stage launches leave no first-task table

@@ -138,10 +138,10 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layouts_match_header():
     from sglang_decode._lib import DecodeArgsC, PlanBuffersC
-    # 25 pointers, scale + pad, 13 int64 strides, 10 int32
-    assert ctypes.sizeof(DecodeArgsC) == 25 * 8 + 8 + 13 * 8 + 10 * 4
-    assert DecodeArgsC.q_stride.offset == 25 * 8 + 8
-    assert ctypes.sizeof(PlanBuffersC) == 21 * 8 + 8 * 4
+    # 26 pointers, scale + pad, 13 int64 strides, 10 int32
+    assert ctypes.sizeof(DecodeArgsC) == 26 * 8 + 8 + 13 * 8 + 10 * 4
+    assert DecodeArgsC.q_stride.offset == 26 * 8 + 8
+    assert ctypes.sizeof(PlanBuffersC) == 22 * 8 + 8 * 4
 
 
 def test_host_static_lists_cpp_matches_reference(plan_vectors):
@@ -185,14 +185,19 @@ def test_attention_kernel_selection_is_host_only():
     args.max_splits, args.page_size, args.csr, args.workers = 16, 1, 1, 256
     args.k_stride[:] = [1024, 0, 128, 1]
     args.v_stride[:] = [1024, 0, 128, 1]
-    for forced in ("generic", "valu", "stream"):
+    for forced in ("generic", "valu", "stream", "mfma"):
         args.kernel = _lib.KERNELS[forced]
         assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == forced
-    args.query_heads = 64  # group 8: no VALU / stream kernel
+    args.query_heads = 64  # group 8: no VALU / stream kernel, the MFMA one serves it
     for forced in ("valu", "stream"):
         args.kernel = _lib.KERNELS[forced]
         assert lib.sgd_attention_kernel(ctypes.byref(args)) == -22
         assert b"group <= 4" in lib.sgd_last_error()
+    args.kernel = _lib.KERNELS["mfma"]
+    assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "mfma"
+    args.head_dim = 64  # head_dim 64: only the generic kernel
+    assert lib.sgd_attention_kernel(ctypes.byref(args)) == -22
+    args.kernel, args.head_dim = _lib.KERNELS["auto"], 128
     args.query_heads, args.kernel = 32, _lib.KERNELS["stream"]
     args.partial = (1 << 20) + 4  # the stream kernel stores partial rows 16 bytes at a time
     assert lib.sgd_attention_kernel(ctypes.byref(args)) == -22
