@@ -61,9 +61,8 @@ int check_args(const sgd_decode_args *args) {
     if (a.csr && (a.page_size != 1 || !a.indptr)) return einval("persistent_decode: CSR needs page_size 1 + indptr");
     if (!a.q || !a.k || !a.v || !a.pages || !a.partial || !a.lse || !a.counter)
         return einval("persistent_decode: null buffer");
-    if (a.dispatch0 && a.dispatch_workers != a.workers)
-        return einval("persistent_decode: dispatch0 holds %d workers' first tasks, the launch has %d",
-                      a.dispatch_workers, a.workers);
+    if (a.dispatch && a.dispatch_units < 0)
+        return einval("persistent_decode: dispatch_units %d < 0", a.dispatch_units);
     return 0;
 }
 

@@ -52,87 +52,103 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// This worker's first task as resolved by the plan (sgd_plan_buffers.dispatch0), when
-// the launch may use it: modes R1, D1, D4, and a table built for this mode and worker
-// count (entry 0's tag).  The host guarantees dispatch0 has an entry per worker.
-struct FirstTask {
-    bool valid;
-    int32_t task, count;
+// ---------------------------------------------------------------- dispatch units
+// A worker's stream of work is a sequence of units: a task in modes R0, R1 and STATIC,
+// a pack of consecutive tasks (pack_first / pack_count) in D1/D4.  The plan's dispatch
+// table (sgd_decode_args.dispatch, written by sgd_build_plan) holds one entry per unit
+// with its first task's record already resolved: {first task, tasks, request, split,
+// begin, end, kv group, kind}.  kind says what the units are -- kTableTasks (task t,
+// record t / Hkv: R1 and STATIC) or kTablePacks -- and an entry is used only when it
+// matches the launch's mode, so a unit resolves in one round trip instead of the
+// pack -> order -> record walk.
+constexpr int32_t kTableTasks = 1, kTablePacks = 2;
+
+__device__ __forceinline__ int32_t table_kind(int32_t mode) {
+    return mode == 1 || mode == 2 ? kTableTasks : mode >= 3 ? kTablePacks : 0;
+}
+
+struct Entry {
+    int4 x, y;  // {first task, tasks, request, split}, {begin, end, group, kind}
+};
+
+// Uniform load of unit u's entry through the scalar cache: the table is written by an
+// earlier launch and never during this one.
+__device__ __forceinline__ Entry load_entry(const int32_t *table, int32_t u) {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    typedef const __attribute__((address_space(4))) v4i cv4i;
+    cv4i *p = (cv4i *)(table + 8 * (int64_t)__builtin_amdgcn_readfirstlane(u));
+    const v4i x = p[0], y = p[1];
+    return Entry{make_int4(x.x, x.y, x.z, x.w), make_int4(y.x, y.y, y.z, y.w)};
+}
+
+struct Unit {
+    int32_t first, count;
+    bool resolved;  // info holds task `first`'s record
     TaskInfo info;
 };
 
-__device__ __forceinline__ FirstTask first_task(const sgd_decode_args &a, int32_t mode) {
-    FirstTask f;
-    f.valid = false;
-    if (!a.dispatch0) return f;
-    const int32_t *e = a.dispatch0 + 8 * blockIdx.x;  // loaded with the tag, in one round trip
-    const int32_t tag = a.dispatch0[7];
-    f.task = e[0];
-    f.count = e[1];
-    f.info.request = e[2];
-    f.info.split = e[3];
-    f.info.start = e[4];
-    f.info.end = e[5];
-    f.info.group = e[6];
-    f.valid = (mode == 1 || mode == 3 || mode == 4) && tag == mode + 8 * a.workers;
-    return f;
+__device__ __forceinline__ Unit unit_of(const sgd_decode_args &a, int32_t u, int32_t mode, bool loaded,
+                                        const Entry &e) {
+    Unit r;
+    if (loaded && e.y.w == table_kind(mode)) {
+        r.first = e.x.x;
+        r.count = e.x.y;
+        r.resolved = true;
+        r.info.request = e.x.z;
+        r.info.split = e.x.w;
+        r.info.start = e.y.x;
+        r.info.end = e.y.y;
+        r.info.group = e.y.z;
+    } else {
+        r.first = mode >= 3 ? __builtin_amdgcn_readfirstlane(a.pack_first[u]) : u;
+        r.count = mode >= 3 ? __builtin_amdgcn_readfirstlane(a.pack_count[u]) : 1;
+        r.resolved = false;
+    }
+    return r;
 }
 
-// Runs `run(task, mode, pre)` for every task of this worker, where pre is the task's
-// resolved TaskInfo when the plan supplied it (the first task; null otherwise).  All
-// threads of the workgroup execute it uniformly; `sh_cursor` is one int of LDS.  With
-// a first-task table in D1/D4, worker w runs pack w first and its claims are
-// workers + (counter): every pack still runs exactly once.
+// Runs `run(task, info)` for every task of this worker, info being the task's record
+// (from the dispatch table for a unit's first task, else decode_task).  All threads of
+// the workgroup execute it uniformly; `sh_cursor` is one int of LDS.  In D1/D4 worker
+// w runs pack w first and its claims return workers + (counter): every pack still
+// runs exactly once.  The next unit is taken when the current one is done (a claim
+// made earlier, while a task streams, holds work back from workers that free up first
+// and measured slower).
 template <class Run>
 __device__ void for_each_task(const sgd_decode_args &a, int32_t *sh_cursor, Run &&run) {
     const int32_t worker = blockIdx.x;
-    const int32_t mode = *a.mode;
-    const FirstTask first = first_task(a, mode);
-    const int32_t total = *a.record_count * a.kv_heads;
+    const int32_t mode = __builtin_amdgcn_readfirstlane(*a.mode);
+    const int32_t total = __builtin_amdgcn_readfirstlane(*a.record_count) * a.kv_heads;
     const bool dynamic = mode >= 3;
-    const int32_t claim_base = (dynamic && first.valid) ? a.workers : 0;
+    const int32_t limit = dynamic ? __builtin_amdgcn_readfirstlane(*a.num_packs) : total;
+    const bool table = a.dispatch != nullptr && mode != 0;
+    const int32_t claim_base = dynamic ? a.workers : 0;
+
     auto claim = [&]() {
         if (threadIdx.x == 0)
             *sh_cursor = claim_base + __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
-        const int32_t c = *sh_cursor;
+        const int32_t c = __builtin_amdgcn_readfirstlane(*sh_cursor);
         __syncthreads();  // every thread has read the claim before the next one overwrites it
         return c;
     };
-    int32_t cursor, limit;
-    if (dynamic) {
-        limit = *a.num_packs;
-        if (first.valid) {
-            if (first.task >= 0) {
-                for (int32_t i = 0; i < first.count; ++i) run(first.task + i, mode, i == 0 ? &first.info : nullptr);
-            }
+
+    int32_t unit = mode == 2 ? __builtin_amdgcn_readfirstlane(a.static_head[worker]) : worker;
+    while (unit >= 0 && unit < limit) {
+        const bool loaded = table && unit < a.dispatch_units;
+        Entry e{};
+        if (loaded) e = load_entry(a.dispatch, unit);
+        const Unit u = unit_of(a, unit, mode, loaded, e);
+        for (int32_t i = 0; i < u.count; ++i) {
+            TaskInfo ti = (i == 0 && u.resolved) ? u.info : decode_task(a, u.first + i, mode);
+            ti.request = __builtin_amdgcn_readfirstlane(ti.request);
+            ti.split = __builtin_amdgcn_readfirstlane(ti.split);
+            ti.start = __builtin_amdgcn_readfirstlane(ti.start);
+            ti.end = __builtin_amdgcn_readfirstlane(ti.end);
+            ti.group = __builtin_amdgcn_readfirstlane(ti.group);
+            run(u.first + i, ti);
         }
-        cursor = claim();
-    } else if (mode == 2) {
-        cursor = a.static_head[worker];
-        limit = total;
-    } else {
-        cursor = worker;
-        limit = total;
-        if (first.valid && cursor < limit) {  // R1: task `worker`, already resolved
-            run(cursor, mode, &first.info);
-            cursor += a.workers;
-        }
-    }
-    while (cursor >= 0 && cursor < limit) {
-        int32_t first_t = cursor, count = 1;
-        if (dynamic) {
-            first_t = a.pack_first[cursor];
-            count = a.pack_count[cursor];
-        }
-        for (int32_t i = 0; i < count; ++i) run(first_t + i, mode, (const TaskInfo *)nullptr);
-        if (dynamic) {
-            cursor = claim();
-        } else if (mode == 2) {
-            cursor = a.static_next[cursor];
-        } else {
-            cursor += a.workers;
-        }
+        unit = dynamic ? claim() : mode == 2 ? __builtin_amdgcn_readfirstlane(a.static_next[unit]) : unit + a.workers;
     }
     // The last worker to finish puts the claim counter back to zero for the next
     // launch.  Relaxed is enough: a worker reaches this increment only after its

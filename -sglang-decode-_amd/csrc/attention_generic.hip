@@ -40,8 +40,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_attention_generic(sgd_decode_ar
     const int64_t KP = a.k_stride[0], KT = a.k_stride[1], KH = a.k_stride[2], KD = a.k_stride[3];
     const int64_t VP = a.v_stride[0], VT = a.v_stride[1], VH = a.v_stride[2], VD = a.v_stride[3];
 
-    for_each_task(a, &sh.cursor, [&](int32_t task, int32_t mode, const TaskInfo *pre) {
-        const TaskInfo t = pre ? *pre : decode_task(a, task, mode);
+    for_each_task(a, &sh.cursor, [&](int32_t, const TaskInfo &t) {
         __syncthreads();  // previous task is done with the shared buffers
         for (int i = threadIdx.x; i < GP * D; i += 64 * kWaves) {
             const int j = i / D, d = i % D;

@@ -180,12 +180,15 @@ template <int DT, bool CSR>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_args a) {
     extern __shared__ __align__(16) char dyn_smem[];
     MfmaShared &sh = *reinterpret_cast<MfmaShared *>(dyn_smem);
-    const int lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
+    const int lane0 = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
     const int32_t G = a.query_heads / a.kv_heads;
     const float scale2 = a.scale * kLog2e;
 
-    for_each_task(a, &sh.cursor, [&](int32_t task, int32_t mode, const TaskInfo *pre) {
-        const TaskInfo ti = pre ? *pre : decode_task(a, task, mode);
+    for_each_task(a, &sh.cursor, [&](int32_t, const TaskInfo &ti) {
+        // A laundered lane id per task: the compiler rebuilds the per-lane offsets
+        // each task instead of holding them (64-bit each) live across the task loop.
+        int lane = lane0;
+        asm volatile("" : "+v"(lane));
         Src t;
         t.request = uni(ti.request);
         t.start = uni(ti.start);
@@ -254,7 +257,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
         // wave state to LDS: head n = lane % 16, dims 32j + 8i + b
         den_l += __shfl_xor(den_l, 16, 64);
         den_l += __shfl_xor(den_l, 32, 64);
-        __syncthreads();  // the previous task's combine is done reading shared memory
+        lds_barrier();  // the previous task's combine is done reading shared memory
         {
             const int n = lane & 15, j = lane >> 4;
 #pragma unroll
@@ -268,7 +271,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
                 sh.d[wave][n] = den_l;
             }
         }
-        __syncthreads();
+        lds_barrier();
         for (int x = threadIdx.x; x < G * kD; x += 64 * kWaves) {
             const int h = x / kD, d = x % kD;
             float mm = -INFINITY;

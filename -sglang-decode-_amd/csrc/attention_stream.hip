@@ -352,12 +352,13 @@ __device__ void schedule(StreamShared &sh, const sgd_decode_args &a, int lane) {
     const bool dynamic = mode >= 3;
     const int32_t num_packs = dynamic ? uni(*a.num_packs) : 0;
     const int32_t active = mode == 0 ? uni(*a.active) : 0;
-    // The plan may have resolved this worker's first task (R1, D1/D4): it is published
-    // without the order -> record walk, and in D1/D4 pack `worker` is taken without a
-    // claim; later claims are then W + counter (every pack still runs once).
-    const FirstTask first = first_task(a, mode);
-    bool first_pending = first.valid;
-    const int32_t claim_base = (dynamic && first.valid) ? W : 0;
+    // With the plan's dispatch table, units resolve to their records in one round trip
+    // (R1 and STATIC per lane, D1/D4 for a pack's first task).  In D1/D4 pack `worker`
+    // is taken without a claim; claims then return W + counter (every pack runs once).
+    const bool table = a.dispatch != nullptr && mode != 0;
+    const int32_t kind = table_kind(mode);
+    const int32_t claim_base = dynamic ? W : 0;
+    bool first_pack = dynamic;
     int32_t seq = 0, base = 0;
     int64_t rr = 0;                          // R0/R1: tasks enumerated so far
     int32_t chain = -1;                      // STATIC: last task taken from the list
@@ -365,14 +366,9 @@ __device__ void schedule(StreamShared &sh, const sgd_decode_args &a, int lane) {
     for (;;) {
         // 1. enumerate up to 64 tasks, one per lane
         int32_t t = -1, nb = 0;
-        bool pre0 = false;  // lane 0's task is the plan-resolved first task
-        if (mode == 1 && first_pending) {
-            first_pending = false;
-            pre0 = first.task >= 0;
-            nb = pre0 ? 1 : 0;
-            t = pre0 && lane == 0 ? first.task : -1;
-            rr = 1;
-        } else if (mode <= 1) {
+        bool pre0 = false;  // lane 0's task was resolved by the pack's table entry
+        TaskInfo p0{};
+        if (mode <= 1) {
             const int64_t tt = (int64_t)blockIdx.x + (rr + lane) * W;
             t = tt < total ? (int32_t)tt : -1;
             const int64_t left = total > (int64_t)blockIdx.x + rr * W
@@ -387,22 +383,30 @@ __device__ void schedule(StreamShared &sh, const sgd_decode_args &a, int lane) {
                 nb = 1;
             }
         } else {
-            if (first_pending) {
-                first_pending = false;
-                if (first.task >= 0) {
-                    pack_next = first.task;
-                    pack_left = first.count;
-                    pre0 = true;
+            if (pack_left == 0) {
+                int32_t c = blockIdx.x;
+                if (first_pack) {
+                    first_pack = false;
+                } else {
+                    // claim only when fewer than kQueueTiles published tiles are unreserved
+                    while (base - lds_acquire(&sh.next_tile) >= kQueueTiles) __builtin_amdgcn_s_sleep(2);
+                    c = 0;
+                    if (lane == 0) c = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    c = claim_base + uni(c);
                 }
-            } else if (pack_left == 0) {
-                // claim only when fewer than kQueueTiles published tiles are unreserved
-                while (base - lds_acquire(&sh.next_tile) >= kQueueTiles) __builtin_amdgcn_s_sleep(2);
-                int32_t c = 0;
-                if (lane == 0) c = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                c = claim_base + uni(c);
                 if (c >= 0 && c < num_packs) {
-                    pack_next = uni(a.pack_first[c]);
-                    pack_left = max(uni(a.pack_count[c]), 0);
+                    const bool use = table && c < a.dispatch_units;
+                    Entry e{};
+                    if (use) e = load_entry(a.dispatch, c);
+                    if (use && e.y.w == kind) {
+                        pack_next = e.x.x;
+                        pack_left = max(e.x.y, 0);
+                        pre0 = true;
+                        p0 = TaskInfo{e.x.z, e.x.w, e.y.x, e.y.y, e.y.z};
+                    } else {
+                        pack_next = uni(a.pack_first[c]);
+                        pack_left = max(uni(a.pack_count[c]), 0);
+                    }
                 }
             }
             nb = min(pack_left, 64);
@@ -415,33 +419,48 @@ __device__ void schedule(StreamShared &sh, const sgd_decode_args &a, int lane) {
         // 2. resolve each lane's task (kernels/attention.py:23-47)
         int32_t request = 0, split = 0, start = 0, end = 0, group = 0, ind0 = 0;
         if (pre0 && lane == 0) {
-            request = first.info.request;
-            split = first.info.split;
-            start = first.info.start;
-            end = first.info.end;
-            group = first.info.group;
+            request = p0.request;
+            split = p0.split;
+            start = p0.start;
+            end = p0.end;
+            group = p0.group;
             if constexpr (CSR) ind0 = a.indptr[request];
         } else if (lane < nb && t >= 0) {
-            group = t % hkv;
-            int32_t rec = t / hkv;
-            if (mode == 0) {
-                int32_t lo = 0, hi = active;
-                while (lo < hi) {
-                    const int32_t mid = (lo + hi) >> 1;
-                    if (rec >= a.offsets[mid + 1]) lo = mid + 1;
-                    else hi = mid;
-                }
-                request = lo;
-                split = rec - a.offsets[lo];
-                const int32_t c = a.chunk[lo];
-                start = split * c;
-                end = min(start + c, a.lengths[lo]);
+            const int4 *ep = reinterpret_cast<const int4 *>(a.dispatch + 8 * (int64_t)t);
+            int4 ex = make_int4(0, 0, 0, 0), ey = make_int4(0, 0, 0, 0);
+            const bool per_task = table && mode <= 2 && t < a.dispatch_units;
+            if (per_task) {
+                ex = ep[0];
+                ey = ep[1];
+            }
+            if (per_task && ey.w == kind) {
+                request = ex.z;
+                split = ex.w;
+                start = ey.x;
+                end = ey.y;
+                group = ey.z;
             } else {
-                if (mode != 2) rec = a.order[rec];
-                request = a.request[rec];
-                split = a.split[rec];
-                start = a.begin[rec];
-                end = a.end[rec];
+                group = t % hkv;
+                int32_t rec = t / hkv;
+                if (mode == 0) {
+                    int32_t lo = 0, hi = active;
+                    while (lo < hi) {
+                        const int32_t mid = (lo + hi) >> 1;
+                        if (rec >= a.offsets[mid + 1]) lo = mid + 1;
+                        else hi = mid;
+                    }
+                    request = lo;
+                    split = rec - a.offsets[lo];
+                    const int32_t c = a.chunk[lo];
+                    start = split * c;
+                    end = min(start + c, a.lengths[lo]);
+                } else {
+                    if (mode != 2) rec = a.order[rec];
+                    request = a.request[rec];
+                    split = a.split[rec];
+                    start = a.begin[rec];
+                    end = a.end[rec];
+                }
             }
             if constexpr (CSR) ind0 = a.indptr[request];
         }

@@ -49,16 +49,17 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
     // VGPRs).
     extern __shared__ __align__(16) char dyn_smem[];
     ValuShared<kWaves> &sh = *reinterpret_cast<ValuShared<kWaves> *>(dyn_smem);
-    const int lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
+    const int lane0 = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
     WaveTile &wt = sh.w[wave];
     const int32_t G = a.query_heads / a.kv_heads;
     const float scale2 = a.scale * kLog2e;
     const int page_shift = __builtin_ctz((unsigned)a.page_size);  // page_size is a power of two here
     const int32_t page_mask = a.page_size - 1;
 
-    for_each_task(a, &sh.cursor, [&](int32_t task, int32_t mode, const TaskInfo *pre) {
-        const TaskInfo ti = pre ? *pre : decode_task(a, task, mode);
-        __syncthreads();  // the previous task's merge is done with shared memory
+    for_each_task(a, &sh.cursor, [&](int32_t, const TaskInfo &ti) {
+        int lane = lane0;  // laundered per task: per-lane offsets are rebuilt, not held live
+        asm volatile("" : "+v"(lane));
+        lds_barrier();  // the previous task's merge is done with shared memory
         if (wave == 0) {  // stage the group's q rows; heads >= G are zero
             const int h = lane >> 4, c = lane & 15;
             uint4 w = make_uint4(0, 0, 0, 0);
@@ -86,7 +87,7 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
         T.vp = a.v_stride[0] * 2;
         T.vt = a.v_stride[1] * 2;
         const int32_t ntiles = (T.end - T.start + kTile - 1) / kTile;
-        __syncthreads();
+        lds_barrier();
 
         const int32_t n0 = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
         uint4 kr[kRowsLoads], vr[kRowsLoads];
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
             sh.cm[wave][lane] = mv;
             sh.cd[wave][lane] = dv;
         }
-        __syncthreads();
+        lds_barrier();
         if (threadIdx.x < kHeads * kD) {  // one (head, dim) output per thread: 4 heads x 128 dims
             static_assert(kWaves * 64 >= kHeads * kD, "merge maps one thread per output");
             const int h = threadIdx.x / kD, d = threadIdx.x % kD;

@@ -60,6 +60,14 @@ __device__ __forceinline__ float round_to(float f) {
     return to_f32<DT>(from_f32<DT>(f));
 }
 
+// Workgroup barrier that orders LDS only: unlike __syncthreads() it does not wait for
+// the waves' outstanding global loads and stores (prefetches stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

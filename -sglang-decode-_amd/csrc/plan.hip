@@ -43,7 +43,7 @@ struct PlanShared {
 // ---------------------------------------------------------------- count/scan
 // Optional LDS copies of the per-row values for the fused kernel's later stages.
 struct RowMirror {
-    int32_t *lengths, *counts, *offsets, *chunk;  // LDS, [bcap] ([bcap + 1] for offsets)
+    int32_t *lengths, *counts, *offsets, *chunk;  // LDS, [bcap] ([bcap + 1] for offsets); counts may be null
 };
 
 constexpr int kMaxRowsPerThread = 4;  // bcap <= 4096 = 4 x kPlanThreads
@@ -90,7 +90,7 @@ __device__ void stage_count_scan(const int32_t *lengths, const int32_t *splits, 
         counts[r] = n;
         offsets[r] = running;
         if (mirror) {
-            mirror->counts[r] = n;
+            if (mirror->counts) mirror->counts[r] = n;
             mirror->offsets[r] = running;
         }
         running = wadd(running, n);
@@ -100,6 +100,7 @@ __device__ void stage_count_scan(const int32_t *lengths, const int32_t *splits, 
         *record_count = total;
         *error = err ? 1 : 0;
         sh.record_count = total;
+        if (mirror) mirror->offsets[bcap] = total;
     }
 }
 
@@ -114,7 +115,7 @@ __device__ void stage_emit_records(const int32_t *lengths, const int32_t *counts
     const int64_t pairs = (int64_t)bcap * smax;
     for (int64_t p = threadIdx.x; p < pairs; p += kPlanThreads) {
         const int r = (int)(p / smax), s = (int)(p % smax);
-        const int32_t n = counts[r];
+        const int32_t n = counts ? counts[r] : wadd(offsets[r + 1], -offsets[r]);
         if (s >= n) continue;
         const int32_t idx = wadd(offsets[r], s);
         const int32_t c = chunk[r];
@@ -144,7 +145,7 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
                                       int32_t *mode_out, const int32_t *rules, int32_t rule_count,
                                       int32_t force, int32_t hkv, int32_t workers, int32_t buckets,
                                       int32_t record_capacity, PlanShared &sh,
-                                      int32_t *order_mirror = nullptr) {
+                                      int16_t *order_mirror = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int per = (record_capacity + kPlanThreads - 1) / kPlanThreads;
     const int i0 = tid * per;
@@ -243,7 +244,7 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
         for (int q = 0; q < kMaxBuckets; ++q)
             if (q == b) { r = rank[q]; rank[q] = r + 1; }
         order[sh.bucket_record_base[b] + r] = i;
-        if (order_mirror) order_mirror[sh.bucket_record_base[b] + r] = i;
+        if (order_mirror) order_mirror[sh.bucket_record_base[b] + r] = (int16_t)i;
     }
     for (int b = buckets - 1; b >= 0; --b) {
         const int32_t count = sh.bucket_pack_count[b], width = sh.bucket_width[b];
@@ -343,46 +344,57 @@ __device__ void stage_greedy_lists(const int32_t *weight, int32_t total, int32_t
     }
 }
 
-// ---------------------------------------------------------------- first tasks
-// Each worker's first task for the attention launch (R1: task w; D1/D4: the first task
-// of pack w, which the launch then assigns to worker w instead of claiming it), with
-// its record resolved: {task, tasks in the pack, request, split, begin, end, group,
-// mode + 8 * workers}.  Pack w is located from the bucket tables in sh exactly as
-// stage_order_and_packs lays the packs out; order comes from its LDS mirror.  The record
-// fields are re-read from global memory (written by this workgroup before a barrier).
-__device__ void stage_dispatch0(int32_t *out, const int32_t *order_mirror, const int32_t *request,
-                                const int32_t *split, const int32_t *begin, const int32_t *end, int32_t total,
-                                int32_t hkv, int32_t workers, int32_t buckets, const PlanShared &sh) {
+// ---------------------------------------------------------------- dispatch table
+// One entry per dispatch unit with its record resolved, so an attention launch goes
+// from a unit straight to its rows: {first task, tasks in the unit, request, split,
+// begin, end, kv group, kind}.  Units follow the mode the plan chose: tasks for R1
+// and STATIC (kind 1, task t is record t / Hkv: STATIC reads records directly and
+// R1's order is the identity, kernels/attention.py:41-47), packs for D1/D4 (kind 2,
+// pack u located in the bucket tables exactly as stage_order_and_packs lays the packs
+// out, its first record through the order).  Nothing is written for R0.  Everything
+// comes from LDS:
+// record rec is (r, rec - offsets[r]) for the request r whose offsets bracket it,
+// with begin and end computed as stage_emit_records computes them.
+__device__ __forceinline__ int32_t request_of(const int32_t *offsets, int32_t bcap, int32_t rec) {
+    int32_t lo = 0, hi = bcap;  // upper bound of rec in offsets[1 .. bcap]
+    while (lo < hi) {
+        const int32_t mid = (lo + hi) >> 1;
+        if (rec >= offsets[mid + 1]) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+__device__ void stage_dispatch_table(int32_t *table, int32_t capacity, const int16_t *order_mirror,
+                                     const RowMirror &rows, int32_t bcap, int32_t total, int32_t hkv,
+                                     int32_t buckets, const PlanShared &sh) {
     const int32_t mode = sh.mode;
-    for (int w = threadIdx.x; w < workers; w += kPlanThreads) {
-        int32_t task = -1, count = 0, rec = -1;
-        if (mode == 1) {
-            if (w < total * hkv) {
-                task = w;
-                count = 1;
-                rec = w / hkv;  // mode 1 writes the identity order
-            }
-        } else if ((mode == 3 || mode == 4) && w < sh.num_packs) {
+    auto write = [&](int32_t unit, int32_t task, int32_t count, int32_t rec, int32_t kind) {
+        if (unit >= capacity) return;
+        const int32_t r = request_of(rows.offsets, bcap, rec);
+        const int32_t s = wadd(rec, -rows.offsets[r]);
+        const int32_t c = rows.chunk[r];
+        const int32_t b = wmul(s, c);
+        int32_t *e = table + 8 * (int64_t)unit;
+        *reinterpret_cast<int4 *>(e) = make_int4(task, count, r, s);
+        *reinterpret_cast<int4 *>(e + 4) = make_int4(b, min(wadd(b, c), rows.lengths[r]), task % hkv, kind);
+    };
+    if (mode == 1 || mode == 2) {
+        for (int32_t i = threadIdx.x; i < total; i += kPlanThreads)
+            for (int32_t g = 0; g < hkv; ++g) write(i * hkv + g, i * hkv + g, 1, i, 1);
+    } else if (mode >= 3) {
+        for (int32_t u = threadIdx.x; u < sh.num_packs; u += kPlanThreads) {
             for (int b = buckets - 1; b >= 0; --b) {
-                const int32_t p = w - sh.bucket_pack_base[b];
+                const int32_t p = u - sh.bucket_pack_base[b];
                 if (p < 0 || p >= sh.bucket_pack_count[b]) continue;
                 const int32_t width = sh.bucket_width[b], pp = sh.bucket_packed_packs[b];
                 const bool packed = p < pp;
-                task = sh.bucket_record_base[b] * hkv + (packed ? p * width : sh.bucket_packed_tasks[b] + p - pp);
-                count = packed ? width : 1;
-                rec = order_mirror[task / hkv];
+                const int32_t first =
+                    sh.bucket_record_base[b] * hkv + (packed ? p * width : sh.bucket_packed_tasks[b] + p - pp);
+                write(u, first, packed ? width : 1, order_mirror[first / hkv], 2);
                 break;
             }
         }
-        int32_t *e = out + 8 * w;
-        e[0] = task;
-        e[1] = count;
-        e[2] = rec >= 0 ? request[rec] : 0;
-        e[3] = rec >= 0 ? split[rec] : 0;
-        e[4] = rec >= 0 ? begin[rec] : 0;
-        e[5] = rec >= 0 ? end[rec] : 0;
-        e[6] = task >= 0 ? task % hkv : 0;
-        e[7] = mode + 8 * workers;
     }
 }
 
@@ -425,20 +437,21 @@ __global__ __launch_bounds__(kPlanThreads) void k_greedy_lists(const int32_t *we
                        g.tail);
 }
 
-// Dynamic LDS of the fused kernel.  Region A holds the per-row values between
-// count/scan and record emission, then the order (for the first-task stage), then the
-// LPT loads/tails; region B holds the record weights between emission, ordering and the
-// LPT, where they become the sort keys.
+// Dynamic LDS of the fused kernel.  Region A holds the per-row values (lengths,
+// offsets, chunks) from count/scan through the dispatch table, then the LPT
+// loads/tails; the order mirror (int16: records < 16384) serves the dispatch table;
+// region B holds the record weights between emission, ordering and the LPT, where they
+// become the sort keys.
 struct FusedLds {
     union {
         struct {
-            int32_t lengths[4096], counts[4096], offsets[4096], chunk[4096];
+            int32_t lengths[4096], offsets[4097], chunk[4096];
         } rows;
-        int32_t order[kGreedyMaxRecords];
         struct {
             int32_t load[kGreedyMaxWorkers], tail[kGreedyMaxWorkers];
         } lpt;
     } a;
+    int16_t order[kGreedyMaxRecords];
     union {
         int32_t weight[kGreedyMaxRecords];
         uint32_t keys[kGreedyMaxRecords];
@@ -454,7 +467,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p,
     extern __shared__ __align__(16) char dyn[];
     FusedLds &L = *reinterpret_cast<FusedLds *>(dyn);
     for (int i = threadIdx.x; i < num_counters; i += kPlanThreads) zero_counters[i] = 0;
-    const RowMirror mirror{L.a.rows.lengths, L.a.rows.counts, L.a.rows.offsets, L.a.rows.chunk};
+    const RowMirror mirror{L.a.rows.lengths, nullptr, L.a.rows.offsets, L.a.rows.chunk};
     stage_count_scan(p.lengths, p.splits, p.active, p.counts, p.offsets, p.chunk, p.record_count, p.error,
                      p.batch_capacity, p.max_splits, p.max_context, sh, &mirror);
     if (force == 0) {  // forced R0: counts/offsets only (planning/builder.py:11-14)
@@ -463,18 +476,16 @@ __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p,
     }
     __syncthreads();
     const int32_t total = sh.record_count;
-    stage_emit_records(L.a.rows.lengths, L.a.rows.counts, L.a.rows.offsets, L.a.rows.chunk, p.request, p.split,
-                       p.begin, p.end, p.weight, p.batch_capacity, p.max_splits, p.block_kv, L.b.weight);
+    stage_emit_records(L.a.rows.lengths, nullptr, L.a.rows.offsets, L.a.rows.chunk, p.request, p.split, p.begin,
+                       p.end, p.weight, p.batch_capacity, p.max_splits, p.block_kv, L.b.weight);
     __syncthreads();
-    // region A (the row values) is free after emission: it takes the order mirror
-    int32_t *order_mirror = L.a.order;
     stage_order_and_packs(L.b.weight, total, p.order, p.pack_first, p.pack_count, p.num_packs, p.mode, p.rules,
                           p.rule_count, force, p.kv_heads, p.workers, p.buckets, p.batch_capacity * p.max_splits,
-                          sh, order_mirror);
-    if (p.dispatch0) {
+                          sh, L.order);
+    if (p.dispatch) {
         __syncthreads();
-        stage_dispatch0(p.dispatch0, order_mirror, p.request, p.split, p.begin, p.end, total, p.kv_heads,
-                        p.workers, p.buckets, sh);
+        stage_dispatch_table(p.dispatch, p.batch_capacity * p.max_splits * p.kv_heads, L.order, mirror,
+                             p.batch_capacity, total, p.kv_heads, p.buckets, sh);
     }
     if (run_greedy) {
         __syncthreads();

@@ -25,7 +25,7 @@ class PlanBuffersC(ctypes.Structure):
     _fields_ = [(name, _P) for name in (
         "lengths", "splits", "active", "counts", "offsets", "chunk", "request", "split", "begin",
         "end", "weight", "order", "pack_first", "pack_count", "record_count", "num_packs", "mode",
-        "error", "static_head", "static_next", "rules", "dispatch0")] + [
+        "error", "static_head", "static_next", "rules", "dispatch")] + [
         (name, _I) for name in ("rule_count", "batch_capacity", "max_splits", "max_context",
                                 "kv_heads", "workers", "block_kv", "buckets")]
 
@@ -35,12 +35,12 @@ class DecodeArgsC(ctypes.Structure):
         "q", "k", "v", "pages", "indptr", "lengths", "request", "split", "begin", "end", "order",
         "offsets", "chunk", "active", "record_count", "mode", "pack_first", "pack_count",
         "num_packs", "counter", "done_counter", "static_head", "static_next", "partial", "lse",
-        "dispatch0")] + [
+        "dispatch")] + [
         ("scale", ctypes.c_float), ("_pad0", _I),
         ("q_stride", ctypes.c_int64 * 3), ("k_stride", ctypes.c_int64 * 4),
         ("v_stride", ctypes.c_int64 * 4), ("pt_stride", ctypes.c_int64 * 2)] + [
         (name, _I) for name in ("query_heads", "kv_heads", "head_dim", "max_splits", "page_size",
-                                "csr", "dtype", "workers", "kernel", "dispatch_workers")]
+                                "csr", "dtype", "workers", "kernel", "dispatch_units")]
 
 
 _SIGNATURES = {

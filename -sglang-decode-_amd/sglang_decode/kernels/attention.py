@@ -27,7 +27,7 @@ def persistent_decode(plan, layer, q, k, v, pages, indptr, scale, k_strides, v_s
     a.partial = layer.partial.data_ptr()
     a.lse = layer.lse.data_ptr()
     if getattr(plan, "dispatch_valid", False):
-        a.dispatch0, a.dispatch_workers = plan.dispatch0.data_ptr(), plan.dispatch0.shape[0]
+        a.dispatch, a.dispatch_units = plan.dispatch.data_ptr(), plan.dispatch.shape[0]
     a.scale = float(scale)
     a.q_stride[:] = list(q.stride())
     a.k_stride[:] = list(k_strides)

@@ -20,7 +20,7 @@ def build_plan(plan, force_mode=-1, *, fused=True, counters=None):
         K.fused_build(plan, force_mode, run_greedy, counters)
         plan.dispatch_valid = True
         return
-    plan.dispatch_valid = False  # the stage launches do not resolve first tasks
+    plan.dispatch_valid = False  # the stage launches write no dispatch table
     if counters is not None:
         counters.zero_()
     K.count_scan(plan)

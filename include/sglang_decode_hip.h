@@ -102,19 +102,21 @@ typedef struct sgd_plan_buffers {
     int32_t *record_count, *num_packs, *mode, *error; /* [1] each */
     int32_t *static_head, *static_next;               /* [workers], [T] */
     const int32_t *rules;                             /* [max(rule_count,1)][5] */
-    int32_t *dispatch0;                               /* optional [workers][8], see below; may be NULL */
+    int32_t *dispatch;                                /* optional [T][8] dispatch table, see below; may be NULL */
     int32_t rule_count;
     int32_t batch_capacity, max_splits, max_context, kv_heads, workers, block_kv, buckets;
 } sgd_plan_buffers;
 
 /*
- * dispatch0 (no reference counterpart): each worker's first task, resolved by the
- * plan so that an attention launch need not walk order -> record (and, in D1/D4,
- * claim -> pack) before its first loads.  Entry w = {task, tasks in the first pack,
- * request, split, begin, end, kv group, mode + 8 * workers}; task = -1 when the worker
- * has none.  Written by sgd_build_plan for modes R1, D1 and D4 only.  When a launch
- * uses it in D1/D4, worker w runs pack w first and its later claims are
- * workers + (claim counter) -- every pack is still run exactly once.
+ * dispatch (no reference counterpart): one entry per dispatch unit with its first
+ * task's record resolved, so that an attention launch goes from a unit to its rows in
+ * one round trip instead of pack -> order -> record.  Units are tasks in modes R1 and
+ * STATIC (task t), packs in D1/D4 (pack u).  Entry = {first task, tasks in the unit,
+ * request, split, begin, end, kv group, kind}, kind 1 = tasks (record t / Hkv; R1's
+ * order is the identity), 2 = packs.  Written by sgd_build_plan for the mode it plans
+ * (not for R0); a launch uses an entry only when its kind matches the launch's mode
+ * (so a table of an R1 plan serves the STATIC lists installed over it).  The table
+ * must come from the same plan build as the other buffers.
  *
  * Whole plan build in one launch (count/scan, records, order and packs, and,
  * when run_greedy != 0, the STATIC lists).  Same results as the four stage
@@ -140,14 +142,14 @@ typedef struct sgd_decode_args {
     const int32_t *static_head, *static_next;
     float *partial;                 /* [bcap, Hq, smax, D] */
     float *lse;                     /* [bcap, Hq, smax] */
-    const int32_t *dispatch0;       /* optional: sgd_build_plan's dispatch0 of this plan (same workers), or NULL */
+    const int32_t *dispatch;        /* optional: sgd_build_plan's dispatch table of this plan, or NULL */
     float scale;
     int32_t _pad0;
     int64_t q_stride[3], k_stride[4], v_stride[4], pt_stride[2];
     int32_t query_heads, kv_heads, head_dim, max_splits, page_size, csr, dtype, workers;
     int32_t kernel;                 /* enum sgd_kernel */
-    int32_t dispatch_workers;       /* entries in dispatch0 (its plan's workers); must equal workers
-                                       when dispatch0 is set */
+    int32_t dispatch_units;         /* entries in dispatch; units at or beyond it resolve through
+                                       the plan arrays */
 } sgd_decode_args;
 
 /*
@@ -157,7 +159,9 @@ typedef struct sgd_decode_args {
  * (record, kv head); dispatch follows *mode (R0 binary search, R1 stride,
  * STATIC lists, D1/D4 atomic pack claims on *counter).  Writes the normalized
  * partial output and natural-log LSE of every task into its (request, q head,
- * split) slot.
+ * split) slot.  In D1/D4 worker w runs pack w first (the plan's first wave of
+ * packs) and its claims return workers + (counter value): every pack still runs
+ * exactly once.
  */
 int sgd_persistent_decode(const sgd_decode_args *args, void *stream);
 

@@ -123,31 +123,29 @@ def test_fused_plan_clears_counters():
     assert counters.tolist() == [0] * 5
 
 
-def expected_dispatch0(ref, c, mode):
-    """Each worker's first task from the oracle plan: R1 task w, D1/D4 the first task
-    of pack w, with its record fields."""
-    hkv, workers = c.kv_heads, c.workers
+def expected_table(ref, c, mode):
+    """The dispatch table from the oracle plan: R1/STATIC task t (record t / Hkv; R1's
+    order is the identity), D1/D4 pack u (its first task's record through the order)."""
+    hkv = c.kv_heads
     total = ref["record_count"] * hkv
-    rows = []
-    for w in range(workers):
-        task, count = -1, 0
-        if mode == 1 and w < total:
-            task, count = w, 1
-        elif mode in (3, 4) and w < ref["num_packs"]:
-            task, count = ref["pack_first"][w], ref["pack_count"][w]
-        if task >= 0:
-            rec = ref["order"][task // hkv]
-            fields = [ref[k][rec] for k in ("request", "split", "begin", "end")]
-        else:
-            fields = [0, 0, 0, 0]
-        rows.append([task, count] + fields + [task % hkv if task >= 0 else 0, mode + 8 * workers])
-    return rows
+    fields = lambda rec: [ref[k][rec] for k in ("request", "split", "begin", "end")]
+    if mode in (1, 2):
+        if mode == 1:
+            assert ref["order"][:ref["record_count"]] == list(range(ref["record_count"]))
+        return [[t, 1] + fields(t // hkv) + [t % hkv, 1] for t in range(total)]
+    if mode in (3, 4):
+        rows = []
+        for u in range(ref["num_packs"]):
+            first, count = ref["pack_first"][u], ref["pack_count"][u]
+            rows.append([first, count] + fields(ref["order"][first // hkv]) + [first % hkv, 2])
+        return rows
+    return []
 
 
-@pytest.mark.parametrize("force", [1, 3, 4])
-def test_first_task_table_matches_oracle(force):
-    """sgd_build_plan's dispatch0: each worker's first task, resolved exactly as the
-    attention dispatch would resolve it (task -> order -> record)."""
+@pytest.mark.parametrize("force", [0, 1, 2, 3, 4])
+def test_dispatch_table_matches_oracle(force):
+    """sgd_build_plan's dispatch table: one entry per unit, resolved exactly as the
+    attention dispatch resolves it (pack -> order -> record); nothing past the units."""
     for name in ("c1", "c2", "c3", "c5"):
         for workers in (7, 256):
             c = W.config_for(name, workers=workers)
@@ -155,12 +153,15 @@ def test_first_task_table_matches_oracle(force):
             splits = W.split_hints(lengths, c.max_splits)
             plan = PlanBuffers(c, "cuda")
             load(plan, lengths, splits)
-            plan.dispatch0.fill_(-9)
+            plan.dispatch.fill_(-9)
             build_plan(plan, force)
             assert plan.dispatch_valid
             lw = list(lengths) + [0] * (c.batch_capacity - len(lengths))
             sw = list(splits) + [1] * (c.batch_capacity - len(splits))
             ref = OP.full_plan(lw, sw, len(lengths), cfg_ns(c), [], force)
-            assert plan.dispatch0.cpu().tolist() == expected_dispatch0(ref, c, force), (name, workers)
+            exp = expected_table(ref, c, force)
+            got = plan.dispatch.cpu()
+            assert got[:len(exp)].tolist() == exp, (name, workers)
+            assert (got[len(exp):] == -9).all(), (name, workers)
     build_plan(plan, force, fused=False)
-    assert not plan.dispatch_valid  # the stage launches leave no first-task table
+    assert not plan.dispatch_valid  # the stage launches write no dispatch table
