@@ -72,12 +72,13 @@ int resolve_kernel(const sgd_decode_args &a) {
         case SGD_KERNEL_AUTO:
             // The stream kernel is one 1024-thread workgroup per CU: with more workers
             // than CUs they would run in turns, so a two-per-CU kernel takes over --
-            // the MFMA one (also for groups <= 4, heads padded: at the Llama-3-8B
-            // layer it measured 3-4 us faster than the VALU per-task kernel), else the
-            // VALU one, else the generic kernel.
+            // the VALU one for groups <= 4 (1-2% faster than the MFMA kernel, whose
+            // 16 MFMA columns are then three-quarters padding, on the Llama-3-8B
+            // layers measured), else the MFMA one (groups up to 16), else the
+            // generic kernel.
             if (stream_supported(a) && a.workers <= device_cus()) return SGD_KERNEL_STREAM;
-            if (mfma_supported(a)) return SGD_KERNEL_MFMA;
             if (valu_supported(a)) return SGD_KERNEL_VALU;
+            if (mfma_supported(a)) return SGD_KERNEL_MFMA;
             return SGD_KERNEL_GENERIC;
         case SGD_KERNEL_GENERIC:
             return SGD_KERNEL_GENERIC;
