@@ -124,12 +124,12 @@ __device__ void for_each_task(const sgd_decode_args &a, int32_t *sh_cursor, Run 
     const bool table = a.dispatch != nullptr && mode != 0;
     const int32_t claim_base = dynamic ? a.workers : 0;
 
-    auto claim = [&]() {
+    auto claim = [&]() {  // (LDS-only barriers: the task's output stores stay in flight)
         if (threadIdx.x == 0)
             *sh_cursor = claim_base + __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
+        lds_barrier();
         const int32_t c = __builtin_amdgcn_readfirstlane(*sh_cursor);
-        __syncthreads();  // every thread has read the claim before the next one overwrites it
+        lds_barrier();  // every thread has read the claim before the next one overwrites it
         return c;
     };
 

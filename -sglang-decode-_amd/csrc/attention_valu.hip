@@ -59,10 +59,12 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
     for_each_task(a, &sh.cursor, [&](int32_t, const TaskInfo &ti) {
         int lane = lane0;  // laundered per task: per-lane offsets are rebuilt, not held live
         asm volatile("" : "+v"(lane));
-        lds_barrier();  // the previous task's merge is done with shared memory
-        if (wave == 0) {  // stage the group's q rows; heads >= G are zero
+        // Global loads first -- q rows (wave 0), then the request's index base, the first
+        // tile's indices and its K/V rows into registers -- so that they are in flight
+        // across the barriers that hand shared memory over from the previous task.
+        uint4 qrow = make_uint4(0, 0, 0, 0);  // wave 0: head lane / 16, dims 8 (lane % 16) ..; zero past G
+        if (wave == 0) {
             const int h = lane >> 4, c = lane & 15;
-            uint4 w = make_uint4(0, 0, 0, 0);
             if (h < G) {
                 const int32_t qd = (int32_t)a.q_stride[2];
                 const uint16_t *qp = static_cast<const uint16_t *>(a.q) + (int64_t)ti.request * a.q_stride[0] +
@@ -70,9 +72,8 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
                 uint32_t w4[4] = {0, 0, 0, 0};
 #pragma unroll
                 for (int e = 0; e < 8; ++e) w4[e >> 1] |= (uint32_t)qp[e * qd] << (16 * (e & 1));
-                w = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+                qrow = make_uint4(w4[0], w4[1], w4[2], w4[3]);
             }
-            sh.q[h][c] = w;
         }
         TileSrc T;
         T.request = uni(ti.request);
@@ -87,8 +88,6 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
         T.vp = a.v_stride[0] * 2;
         T.vt = a.v_stride[1] * 2;
         const int32_t ntiles = (T.end - T.start + kTile - 1) / kTile;
-        lds_barrier();
-
         const int32_t n0 = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
         uint4 kr[kRowsLoads], vr[kRowsLoads];
         int32_t idx_next = 0;
@@ -97,6 +96,9 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
             tile_issue<CSR>(T, wave, i0, page_mask, lane, kr, vr);
             if (n0 > 1) idx_next = tile_index<CSR>(a, T, T.start + (wave + kWaves) * kTile, lane, page_shift);
         }
+        lds_barrier();  // the previous task's merge is done with shared memory
+        if (wave == 0) sh.q[lane >> 4][lane & 15] = qrow;
+        lds_barrier();
         float m_l = -INFINITY, den_l = 0.f;  // this lane's head (QK roles)
         float acc[kHeads][4];
 #pragma unroll

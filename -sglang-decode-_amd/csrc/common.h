@@ -104,9 +104,9 @@ template <typename T>
 __device__ T block_exclusive_scan(T v, T *tmp, T *total) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
     T inc = wave_inclusive_scan(v);
-    __syncthreads();
+    lds_barrier();
     if (lane == 63) tmp[wid] = inc;
-    __syncthreads();
+    lds_barrier();
     T base = 0, sum = 0;
     for (int w = 0; w < nw; ++w) {
         T t = tmp[w];

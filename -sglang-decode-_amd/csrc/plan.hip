@@ -37,7 +37,9 @@ struct PlanShared {
     int32_t record_count;
     int32_t num_packs;
     int32_t max_w, min_w;
-    int32_t red_max[16], red_min[16];
+    int32_t red_max[16], red_min[16], red_or[16];
+    int32_t hist[16][kMaxBuckets];  // per-wave bucket counts of one partition pass
+    int32_t carry[kMaxBuckets];     // bucket counts of the earlier passes
 };
 
 // ---------------------------------------------------------------- count/scan
@@ -65,8 +67,9 @@ __device__ void stage_count_scan(const int32_t *lengths, const int32_t *splits, 
         const int r = r0 + i;
         if (i >= per || r >= bcap) continue;
         const bool live = r < active;
-        const int32_t length = live ? lengths[r] : 0;
-        const int32_t s = live ? splits[r] : 1;
+        const int32_t raw_length = lengths[r], raw_split = splits[r];  // issued with the load of active
+        const int32_t length = live ? raw_length : 0;
+        const int32_t s = live ? raw_split : 1;
         const bool invalid = live && (length < 0 || length > max_context || s < 1 || s > smax);
         invalid_any |= invalid;
         const int32_t c = wmul(cdiv(cdiv(max(length, 0), max(s, 1)), 32), 32);
@@ -78,7 +81,14 @@ __device__ void stage_count_scan(const int32_t *lengths, const int32_t *splits, 
             mirror->chunk[r] = c;
         }
     }
-    const bool err = (active < 0) || (active > bcap) || __syncthreads_or(invalid_any);
+    // workgroup OR of the validity flags through LDS (outputs stay in flight)
+    const bool wave_invalid = __ballot(invalid_any) != 0;
+    if ((tid & 63) == 0) sh.red_or[tid >> 6] = wave_invalid;
+    lds_barrier();
+    bool any_invalid = false;
+#pragma unroll
+    for (int w = 0; w < kPlanThreads / 64; ++w) any_invalid |= sh.red_or[w] != 0;
+    const bool err = (active < 0) || (active > bcap) || any_invalid;
     if (err) local = 0;
     int32_t total;
     int32_t running = block_exclusive_scan<int32_t>(local, sh.scan_tmp, &total);
@@ -137,6 +147,55 @@ __device__ __forceinline__ int bucket_of(int32_t w, int buckets) {
     return b;
 }
 
+// ---------------------------------------------------------------- bucket tables
+// The bucket tables in registers: lane q (< kMaxBuckets) of every wave holds bucket q's
+// entries, so a sorted record position finds its bucket without LDS round trips.
+struct BucketRegs {
+    int32_t rbase, size, pbase, width, pp, pt;
+    __device__ BucketRegs(const PlanShared &sh, int lane) {
+        const int q = lane < kMaxBuckets ? lane : 0;
+        rbase = sh.bucket_record_base[q];
+        size = sh.bucket_size[q];
+        pbase = sh.bucket_pack_base[q];
+        width = sh.bucket_width[q];
+        pp = sh.bucket_packed_packs[q];
+        pt = sh.bucket_packed_tasks[q];
+    }
+};
+
+struct BucketOf {
+    int32_t rbase, pbase, width, pp, pt;
+};
+
+// The bucket holding sorted record position j (buckets are laid out heaviest first).
+__device__ __forceinline__ BucketOf bucket_at(const BucketRegs &R, int32_t j, int buckets) {
+    BucketOf o{0, 0, 1, 0, 0};
+    for (int q = buckets - 1; q >= 0; --q) {
+        const int32_t lo = __builtin_amdgcn_readlane(R.rbase, q), n = __builtin_amdgcn_readlane(R.size, q);
+        if (j >= lo && j < lo + n) {
+            o.rbase = lo;
+            o.pbase = __builtin_amdgcn_readlane(R.pbase, q);
+            o.width = __builtin_amdgcn_readlane(R.width, q);
+            o.pp = __builtin_amdgcn_readlane(R.pp, q);
+            o.pt = __builtin_amdgcn_readlane(R.pt, q);
+        }
+    }
+    return o;
+}
+
+// The pack that task `task` starts (its index, and its task count in `count`), or -1
+// when the task is inside a pack.  Within a bucket the first packed_tasks tasks form
+// packs of `width`, the rest are singletons (make_order_and_packs, kernels/plan.py:48-100).
+__device__ __forceinline__ int32_t pack_of(const BucketOf &o, int32_t task, int32_t hkv, int32_t &count) {
+    const int32_t p = task - o.rbase * hkv;
+    if (p < o.pt) {
+        count = o.width;
+        return p % o.width == 0 ? o.pbase + p / o.width : -1;
+    }
+    count = 1;
+    return o.pbase + o.pp + (p - o.pt);
+}
+
 // ---------------------------------------------------------------- mode, order, packs
 // weight is read through the given pointer (global, or the fused kernel's LDS copy);
 // total = record count.  Leaves the selected mode in sh.mode.
@@ -164,7 +223,7 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
         mn = min(mn, __shfl_xor(mn, o, 64));
     }
     if (lane == 0) { sh.red_max[wid] = mx; sh.red_min[wid] = mn; }
-    __syncthreads();
+    lds_barrier();
     if (tid == 0) {
         int32_t a = 1, b = INT32_MAX;
         for (int w = 0; w < kPlanThreads / 64; ++w) { a = max(a, sh.red_max[w]); b = min(b, sh.red_min[w]); }
@@ -181,7 +240,7 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
         sh.max_w = a;
         *mode_out = mode;
     }
-    __syncthreads();
+    lds_barrier();
     const int32_t mode = sh.mode, max_w = sh.max_w;
     if (mode == 0 || mode == 1) {
         for (int i = tid; i < total; i += kPlanThreads) order[i] = i;
@@ -191,69 +250,97 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
         }
         return;
     }
-    // Stable partition by bucket, heaviest first.  Each thread owns a contiguous
-    // segment; per-bucket counts are packed 4 x 16-bit per uint64 so four block
-    // scans cover 16 buckets (segment counts <= 16, totals <= 16384 < 2^16).
-    // (arrays below are only ever indexed by compile-time constants: no scratch)
-    uint64_t cnt[4] = {0, 0, 0, 0};
-    for (int k = 0; k < per; ++k) {
-        const int i = i0 + k;
-        if (i >= total) break;
-        const int b = bucket_of(weight[i], buckets);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if ((b >> 2) == q) cnt[q] += (uint64_t)1 << (16 * (b & 3));
+    // Stable partition by bucket, heaviest first, in passes of kPlanThreads records
+    // (record i = pass base + thread): each wave ranks its lanes within their bucket by
+    // ballot, and the waves' counts meet in LDS.  First the bucket sizes ...
+    if (tid < kMaxBuckets) {
+        sh.bucket_size[tid] = 0;
+        sh.carry[tid] = 0;
     }
-    uint64_t base[4], tot[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) base[q] = block_exclusive_scan<uint64_t>(cnt[q], sh.scan_tmp64, &tot[q]);
-    if (tid == 0) {
-#pragma unroll
-        for (int b = 0; b < kMaxBuckets; ++b)
-            sh.bucket_size[b] = (int32_t)((tot[b >> 2] >> (16 * (b & 3))) & 0xffff);
-        int32_t rec_base = 0, pack_base = 0;
-        for (int b = buckets - 1; b >= 0; --b) {
-            const int32_t size = sh.bucket_size[b];
-            const int32_t tasks = size * hkv;
-            const int32_t width = (mode == 4) ? min(4, max(1, max_w / (1 << b))) : 1;
-            const int32_t packed_tasks = max(0, tasks - workers) / width * width;
-            const int32_t packed_packs = packed_tasks / width;
-            const int32_t count = packed_packs + tasks - packed_tasks;
+    lds_barrier();
+    for (int p0 = 0; p0 < total; p0 += kPlanThreads) {
+        const int i = p0 + tid;
+        const int b = i < total ? bucket_of(weight[i], buckets) : -1;
+        for (int q = 0; q < buckets; ++q) {
+            const uint64_t m = __ballot(b == q);
+            if (lane == q && m) atomicAdd(&sh.bucket_size[q], (int32_t)__popcll(m));
+        }
+    }
+    lds_barrier();
+    // ... then the bucket tables, lane b of wave 0 for bucket b (bases run over the
+    // heavier buckets b' > b) ...
+    if (wid == 0) {
+        const int b = lane;
+        const bool live = b < buckets;
+        const int32_t size = live ? sh.bucket_size[b] : 0;
+        const int32_t tasks = size * hkv;
+        const int32_t width = (live && mode == 4) ? min(4, max(1, max_w / (1 << b))) : 1;
+        const int32_t packed_tasks = max(0, tasks - workers) / width * width;
+        const int32_t packed_packs = packed_tasks / width;
+        const int32_t count = live ? packed_packs + tasks - packed_tasks : 0;
+        int32_t rec_base = 0, pack_base = 0, packs = 0;
+        for (int q = 0; q < kMaxBuckets; ++q) {
+            const int32_t sq = __builtin_amdgcn_readlane(size, q), cq = __builtin_amdgcn_readlane(count, q);
+            if (q > b) {
+                rec_base += sq;
+                pack_base += cq;
+            }
+            packs += cq;
+        }
+        if (b < kMaxBuckets) {
             sh.bucket_record_base[b] = rec_base;
             sh.bucket_pack_base[b] = pack_base;
             sh.bucket_pack_count[b] = count;
             sh.bucket_width[b] = width;
             sh.bucket_packed_packs[b] = packed_packs;
             sh.bucket_packed_tasks[b] = packed_tasks;
-            rec_base += size;
-            pack_base += count;
         }
-        *num_packs = pack_base;
-        sh.num_packs = pack_base;
+        if (lane == 0) {
+            *num_packs = packs;
+            sh.num_packs = packs;
+        }
     }
-    __syncthreads();
-    int32_t rank[kMaxBuckets];
-#pragma unroll
-    for (int b = 0; b < kMaxBuckets; ++b) rank[b] = (int32_t)((base[b >> 2] >> (16 * (b & 3))) & 0xffff);
-    for (int k = 0; k < per; ++k) {
-        const int i = i0 + k;
-        if (i >= total) break;
-        const int b = bucket_of(weight[i], buckets);
-        int32_t r = 0;
-#pragma unroll
-        for (int q = 0; q < kMaxBuckets; ++q)
-            if (q == b) { r = rank[q]; rank[q] = r + 1; }
-        order[sh.bucket_record_base[b] + r] = i;
-        if (order_mirror) order_mirror[sh.bucket_record_base[b] + r] = (int16_t)i;
+    lds_barrier();
+    // ... then each record's rank: earlier passes, earlier waves, earlier lanes.
+    for (int p0 = 0; p0 < total; p0 += kPlanThreads) {
+        const int i = p0 + tid;
+        const int b = i < total ? bucket_of(weight[i], buckets) : -1;
+        uint64_t same = 0;
+        int32_t lane_count = 0;
+        for (int q = 0; q < buckets; ++q) {
+            const uint64_t m = __ballot(b == q);
+            if (b == q) same = m;
+            if (lane == q) lane_count = (int32_t)__popcll(m);
+        }
+        if (lane < kMaxBuckets) sh.hist[wid][lane] = lane_count;
+        lds_barrier();
+        if (b >= 0) {
+            int32_t r = sh.carry[b] + (int32_t)__popcll(same & ((1ull << lane) - 1));
+            for (int w = 0; w < wid; ++w) r += sh.hist[w][b];
+            const int32_t pos = sh.bucket_record_base[b] + r;
+            order[pos] = i;
+            if (order_mirror) order_mirror[pos] = (int16_t)i;
+        }
+        lds_barrier();
+        if (tid < kMaxBuckets) {
+            int32_t n = 0;
+            for (int w = 0; w < kPlanThreads / 64; ++w) n += sh.hist[w][tid];
+            sh.carry[tid] += n;
+        }
+        lds_barrier();
     }
-    for (int b = buckets - 1; b >= 0; --b) {
-        const int32_t count = sh.bucket_pack_count[b], width = sh.bucket_width[b];
-        const int32_t pp = sh.bucket_packed_packs[b], pt = sh.bucket_packed_tasks[b];
-        const int32_t first0 = sh.bucket_record_base[b] * hkv, out0 = sh.bucket_pack_base[b];
-        for (int p = tid; p < count; p += kPlanThreads) {
-            const bool packed = p < pp;
-            pack_first[out0 + p] = first0 + (packed ? p * width : pt + p - pp);
-            pack_count[out0 + p] = packed ? width : 1;
+    // Pack tables, one sorted record position per thread: its tasks that start a pack.
+    const BucketRegs R(sh, lane);
+    for (int j = tid; j < total; j += kPlanThreads) {
+        const BucketOf o = bucket_at(R, j, buckets);
+        for (int g = 0; g < hkv; ++g) {
+            int32_t count;
+            const int32_t task = j * hkv + g;
+            const int32_t unit = pack_of(o, task, hkv, count);
+            if (unit >= 0) {
+                pack_first[unit] = task;
+                pack_count[unit] = count;
+            }
         }
     }
 }
@@ -293,7 +380,7 @@ __device__ void stage_greedy_lists(const int32_t *weight, int32_t total, int32_t
         g.tail[w] = -1;
         static_head[w] = -1;
     }
-    __syncthreads();
+    __syncthreads();  // also orders the static_head stores before wave 0 rewrites them
     for (int k = 2; k <= n2; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
             for (int i = tid; i < n2; i += kPlanThreads) {
@@ -304,7 +391,7 @@ __device__ void stage_greedy_lists(const int32_t *weight, int32_t total, int32_t
                     if ((a > b) == up) { g.keys[i] = b; g.keys[p] = a; }
                 }
             }
-            __syncthreads();
+            lds_barrier();
         }
     }
     if (tid >= 64) return;
@@ -369,31 +456,25 @@ __device__ void stage_dispatch_table(int32_t *table, int32_t capacity, const int
                                      const RowMirror &rows, int32_t bcap, int32_t total, int32_t hkv,
                                      int32_t buckets, const PlanShared &sh) {
     const int32_t mode = sh.mode;
-    auto write = [&](int32_t unit, int32_t task, int32_t count, int32_t rec, int32_t kind) {
-        if (unit >= capacity) return;
+    if (mode == 0) return;
+    const BucketRegs R(sh, threadIdx.x & 63);
+    // one record per thread: its request found once, then its Hkv tasks
+    for (int32_t j = threadIdx.x; j < total; j += kPlanThreads) {
+        const int32_t rec = mode >= 3 ? (int32_t)order_mirror[j] : j;
         const int32_t r = request_of(rows.offsets, bcap, rec);
         const int32_t s = wadd(rec, -rows.offsets[r]);
         const int32_t c = rows.chunk[r];
         const int32_t b = wmul(s, c);
-        int32_t *e = table + 8 * (int64_t)unit;
-        *reinterpret_cast<int4 *>(e) = make_int4(task, count, r, s);
-        *reinterpret_cast<int4 *>(e + 4) = make_int4(b, min(wadd(b, c), rows.lengths[r]), task % hkv, kind);
-    };
-    if (mode == 1 || mode == 2) {
-        for (int32_t i = threadIdx.x; i < total; i += kPlanThreads)
-            for (int32_t g = 0; g < hkv; ++g) write(i * hkv + g, i * hkv + g, 1, i, 1);
-    } else if (mode >= 3) {
-        for (int32_t u = threadIdx.x; u < sh.num_packs; u += kPlanThreads) {
-            for (int b = buckets - 1; b >= 0; --b) {
-                const int32_t p = u - sh.bucket_pack_base[b];
-                if (p < 0 || p >= sh.bucket_pack_count[b]) continue;
-                const int32_t width = sh.bucket_width[b], pp = sh.bucket_packed_packs[b];
-                const bool packed = p < pp;
-                const int32_t first =
-                    sh.bucket_record_base[b] * hkv + (packed ? p * width : sh.bucket_packed_tasks[b] + p - pp);
-                write(u, first, packed ? width : 1, order_mirror[first / hkv], 2);
-                break;
-            }
+        const int32_t e = min(wadd(b, c), rows.lengths[r]);
+        const BucketOf o = bucket_at(R, j, buckets);
+        for (int32_t g = 0; g < hkv; ++g) {
+            const int32_t task = j * hkv + g;
+            int32_t count = 1, unit = task;
+            if (mode >= 3) unit = pack_of(o, task, hkv, count);
+            if (unit < 0 || unit >= capacity) continue;
+            int32_t *ent = table + 8 * (int64_t)unit;
+            *reinterpret_cast<int4 *>(ent) = make_int4(task, count, r, s);
+            *reinterpret_cast<int4 *>(ent + 4) = make_int4(b, e, g, mode >= 3 ? 2 : 1);
         }
     }
 }
@@ -474,21 +555,21 @@ __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p,
         if (threadIdx.x == 0) { *p.mode = 0; *p.num_packs = 0; }
         return;
     }
-    __syncthreads();
+    lds_barrier();
     const int32_t total = sh.record_count;
     stage_emit_records(L.a.rows.lengths, nullptr, L.a.rows.offsets, L.a.rows.chunk, p.request, p.split, p.begin,
                        p.end, p.weight, p.batch_capacity, p.max_splits, p.block_kv, L.b.weight);
-    __syncthreads();
+    lds_barrier();
     stage_order_and_packs(L.b.weight, total, p.order, p.pack_first, p.pack_count, p.num_packs, p.mode, p.rules,
                           p.rule_count, force, p.kv_heads, p.workers, p.buckets, p.batch_capacity * p.max_splits,
                           sh, L.order);
     if (p.dispatch) {
-        __syncthreads();
+        lds_barrier();
         stage_dispatch_table(p.dispatch, p.batch_capacity * p.max_splits * p.kv_heads, L.order, mirror,
                              p.batch_capacity, total, p.kv_heads, p.buckets, sh);
     }
     if (run_greedy) {
-        __syncthreads();
+        lds_barrier();
         // the LPT's loads and tails take region A (free by now), its keys replace the weights
         stage_greedy_lists(L.b.weight, total, sh.mode, p.static_head, p.static_next, p.kv_heads, p.workers,
                            L.b.keys, L.a.lpt.load, L.a.lpt.tail);
