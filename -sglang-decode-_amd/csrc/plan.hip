@@ -18,6 +18,7 @@ namespace {
 
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxBuckets = 16;
+constexpr int kLdsRules = 32;  // policy rules the fused kernel copies to LDS (more stay in global memory)
 
 __device__ __forceinline__ int32_t wadd(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
 __device__ __forceinline__ int32_t wmul(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
@@ -38,6 +39,7 @@ struct PlanShared {
     int32_t num_packs;
     int32_t max_w, min_w;
     int32_t red_max[16], red_min[16], red_or[16];
+    int32_t rules[5 * kLdsRules];   // the fused kernel's copy of the policy rules
     int32_t hist[16][kMaxBuckets];  // per-wave bucket counts of one partition pass
     int32_t carry[kMaxBuckets];     // bucket counts of the earlier passes
 };
@@ -138,6 +140,40 @@ __device__ void stage_emit_records(const int32_t *lengths, const int32_t *counts
         const int32_t w = cdiv(wadd(e, -b), block_kv);
         weight[idx] = w;
         if (weight_mirror) weight_mirror[idx] = w;
+    }
+}
+
+// The request of record rec: the upper bound of rec in offsets[1 .. bcap] (records of a
+// request are contiguous; empty requests are skipped).
+__device__ __forceinline__ int32_t request_of(const int32_t *offsets, int32_t bcap, int32_t rec) {
+    int32_t lo = 0, hi = bcap;  // upper bound of rec in offsets[1 .. bcap]
+    while (lo < hi) {
+        const int32_t mid = (lo + hi) >> 1;
+        if (rec >= offsets[mid + 1]) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// The fused kernel's emission, one record per thread (work grows with the records, not
+// with bcap x smax): the request of record idx comes from the LDS offsets, the fields
+// are those of stage_emit_records.
+__device__ void stage_emit_by_record(const RowMirror &rows, int32_t total, int32_t bcap, int32_t *request,
+                                     int32_t *split, int32_t *begin, int32_t *end, int32_t *weight,
+                                     int32_t block_kv, int32_t *weight_mirror) {
+    for (int32_t idx = threadIdx.x; idx < total; idx += kPlanThreads) {
+        const int32_t r = request_of(rows.offsets, bcap, idx);
+        const int32_t s = wadd(idx, -rows.offsets[r]);
+        const int32_t c = rows.chunk[r];
+        const int32_t b = wmul(s, c);
+        const int32_t e = min(wadd(b, c), rows.lengths[r]);
+        request[idx] = r;
+        split[idx] = s;
+        begin[idx] = b;
+        end[idx] = e;
+        const int32_t w = cdiv(wadd(e, -b), block_kv);
+        weight[idx] = w;
+        weight_mirror[idx] = w;
     }
 }
 
@@ -439,19 +475,8 @@ __device__ void stage_greedy_lists(const int32_t *weight, int32_t total, int32_t
 // R1's order is the identity, kernels/attention.py:41-47), packs for D1/D4 (kind 2,
 // pack u located in the bucket tables exactly as stage_order_and_packs lays the packs
 // out, its first record through the order).  Nothing is written for R0.  Everything
-// comes from LDS:
-// record rec is (r, rec - offsets[r]) for the request r whose offsets bracket it,
-// with begin and end computed as stage_emit_records computes them.
-__device__ __forceinline__ int32_t request_of(const int32_t *offsets, int32_t bcap, int32_t rec) {
-    int32_t lo = 0, hi = bcap;  // upper bound of rec in offsets[1 .. bcap]
-    while (lo < hi) {
-        const int32_t mid = (lo + hi) >> 1;
-        if (rec >= offsets[mid + 1]) lo = mid + 1;
-        else hi = mid;
-    }
-    return lo;
-}
-
+// comes from LDS: record rec is (request_of(rec), rec - offsets[r]), with begin and end
+// computed as stage_emit_records computes them.
 __device__ void stage_dispatch_table(int32_t *table, int32_t capacity, const int16_t *order_mirror,
                                      const RowMirror &rows, int32_t bcap, int32_t total, int32_t hkv,
                                      int32_t buckets, const PlanShared &sh) {
@@ -548,19 +573,27 @@ __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p,
     extern __shared__ __align__(16) char dyn[];
     FusedLds &L = *reinterpret_cast<FusedLds *>(dyn);
     for (int i = threadIdx.x; i < num_counters; i += kPlanThreads) zero_counters[i] = 0;
+    // The policy rules go to LDS: loaded (one int per thread, index clamped into the
+    // buffer, which holds at least one row) together with count/scan's loads, stored
+    // after it, published by the barrier that follows.
+    static_assert(5 * kLdsRules <= kPlanThreads, "one rule int per thread");
+    const bool rules_lds = p.rule_count <= kLdsRules;
+    const int32_t rule_v = p.rules[min((int)threadIdx.x, 5 * max(p.rule_count, 1) - 1)];
     const RowMirror mirror{L.a.rows.lengths, nullptr, L.a.rows.offsets, L.a.rows.chunk};
     stage_count_scan(p.lengths, p.splits, p.active, p.counts, p.offsets, p.chunk, p.record_count, p.error,
                      p.batch_capacity, p.max_splits, p.max_context, sh, &mirror);
+    if (rules_lds && (int)threadIdx.x < 5 * p.rule_count) sh.rules[threadIdx.x] = rule_v;
     if (force == 0) {  // forced R0: counts/offsets only (planning/builder.py:11-14)
         if (threadIdx.x == 0) { *p.mode = 0; *p.num_packs = 0; }
         return;
     }
     lds_barrier();
     const int32_t total = sh.record_count;
-    stage_emit_records(L.a.rows.lengths, nullptr, L.a.rows.offsets, L.a.rows.chunk, p.request, p.split, p.begin,
-                       p.end, p.weight, p.batch_capacity, p.max_splits, p.block_kv, L.b.weight);
+    stage_emit_by_record(mirror, total, p.batch_capacity, p.request, p.split, p.begin, p.end, p.weight, p.block_kv,
+                         L.b.weight);
     lds_barrier();
-    stage_order_and_packs(L.b.weight, total, p.order, p.pack_first, p.pack_count, p.num_packs, p.mode, p.rules,
+    stage_order_and_packs(L.b.weight, total, p.order, p.pack_first, p.pack_count, p.num_packs, p.mode,
+                          rules_lds ? sh.rules : p.rules,
                           p.rule_count, force, p.kv_heads, p.workers, p.buckets, p.batch_capacity * p.max_splits,
                           sh, L.order);
     if (p.dispatch) {
