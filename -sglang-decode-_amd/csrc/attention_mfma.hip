@@ -107,7 +107,7 @@ __device__ __forceinline__ void tile_issue(const Src &t, int32_t tok0, int32_t i
         if constexpr (!CSR) off += (int64_t)((tok0 + tt) & t.page_mask) * t.kt;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-            r.k[h][c] = *reinterpret_cast<const uint4 *>(t.kbase + off + (32 * c + 8 * j) * 2);
+            r.k[h][c] = load_stream16(t.kbase + off + (32 * c + 8 * j) * 2);
     }
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
@@ -115,7 +115,7 @@ __device__ __forceinline__ void tile_issue(const Src &t, int32_t tok0, int32_t i
         const uint32_t phys = (uint32_t)__shfl(idxv, tt, 64);
         int64_t off = (int64_t)phys * t.vp + m * 16;
         if constexpr (!CSR) off += (int64_t)((tok0 + tt) & t.page_mask) * t.vt;
-        r.v[s] = *reinterpret_cast<const uint4 *>(t.vbase + off);
+        r.v[s] = load_stream16(t.vbase + off);
     }
 }
 

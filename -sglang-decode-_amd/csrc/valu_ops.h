@@ -133,8 +133,8 @@ __device__ __forceinline__ void tile_issue(const TileSrc &t, int32_t tile, int32
             ko += (int64_t)inner * t.kt;                                                             \
             vo += (int64_t)inner * t.vt;                                                             \
         }                                                                                            \
-        kr[I] = *reinterpret_cast<const uint4 *>(t.kbase + ko);                                      \
-        vr[I] = *reinterpret_cast<const uint4 *>(t.vbase + vo);                                      \
+        kr[I] = load_stream16(t.kbase + ko);                                                           \
+        vr[I] = load_stream16(t.vbase + vo);                                                           \
     }
     static_assert(kRowsLoads == 4, "one SGD_LOAD_ROW per 4-row load");
     SGD_LOAD_ROW(0) SGD_LOAD_ROW(1) SGD_LOAD_ROW(2) SGD_LOAD_ROW(3)
