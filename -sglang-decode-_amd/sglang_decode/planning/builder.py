@@ -18,9 +18,9 @@ def build_plan(plan, force_mode=-1, *, fused=True, counters=None):
     run_greedy = force_mode == 2 or any_static_rule(plan)
     if fused:
         K.fused_build(plan, force_mode, run_greedy, counters)
-        plan.dispatch_valid = True
+        plan.dispatch_valid = plan.span_valid = True
         return
-    plan.dispatch_valid = False  # the stage launches write no dispatch table
+    plan.dispatch_valid = plan.span_valid = False  # the stage launches write neither table
     if counters is not None:
         counters.zero_()
     K.count_scan(plan)

@@ -136,12 +136,32 @@ def test_library_exports_every_declared_symbol():
     assert b"gfx950" in handle.sgd_version()
 
 
-def test_struct_layouts_match_header():
+def test_struct_layouts_match_header(tmp_path):
+    """Every ctypes field sits at the offset the C header gives it (gcc prints offsetof
+    for each field of sgd_decode_args and sgd_plan_buffers), and the sizes agree."""
+    import shutil
+    import subprocess
     from sglang_decode._lib import DecodeArgsC, PlanBuffersC
-    # 26 pointers, scale + pad, 13 int64 strides, 10 int32
-    assert ctypes.sizeof(DecodeArgsC) == 26 * 8 + 8 + 13 * 8 + 10 * 4
-    assert DecodeArgsC.q_stride.offset == 26 * 8 + 8
-    assert ctypes.sizeof(PlanBuffersC) == 22 * 8 + 8 * 4
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    include = os.path.join(ROOT, "include")
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "sglang_decode_hip.h"', 'int main(void) {']
+    for cstruct, pystruct in (("sgd_decode_args", DecodeArgsC), ("sgd_plan_buffers", PlanBuffersC)):
+        lines.append(f'printf("{cstruct} size %zu\\n", sizeof({cstruct}));')
+        for name, _ in pystruct._fields_:
+            lines.append(f'printf("{cstruct} {name} %zu\\n", offsetof({cstruct}, {name}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-I", include, str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {tuple(line.split()[:2]): int(line.split()[2]) for line in out if line}
+    for cstruct, pystruct in (("sgd_decode_args", DecodeArgsC), ("sgd_plan_buffers", PlanBuffersC)):
+        assert got[(cstruct, "size")] == ctypes.sizeof(pystruct), cstruct
+        for name, _ in pystruct._fields_:
+            assert got[(cstruct, name)] == getattr(pystruct, name).offset, (cstruct, name)
 
 
 def test_host_static_lists_cpp_matches_reference(plan_vectors):
