@@ -76,16 +76,16 @@ int check_args(const sgd_decode_args *args) {
 int resolve_kernel(const sgd_decode_args &a) {
     switch (a.kernel) {
         case SGD_KERNEL_AUTO:
-            // The span kernel streams every wave's equal share of the step's tiles
-            // with no task boundary in its load stream: the fastest where it applies
-            // (groups <= 4 with the plan's span tables).  Otherwise:
-            // the stream kernel is one 1024-thread workgroup per CU: with more workers
+            // The stream kernel is one 1024-thread workgroup per CU: with more workers
             // than CUs they would run in turns, so a two-per-CU kernel takes over --
             // the VALU one for groups <= 4 (1-2% faster than the MFMA kernel, whose
             // 16 MFMA columns are then three-quarters padding, on the Llama-3-8B
             // layers measured), else the MFMA one (groups up to 16), else the
-            // generic kernel.
-            if (span_supported(a)) return SGD_KERNEL_SPAN;
+            // generic kernel.  The span kernel runs on request only: on the
+            // Llama-3-8B batch-64 layer its static equal shares end unevenly within a
+            // workgroup (the waves' latencies differ), and with its edge-completing
+            // merge the layer takes 82.2 us against 76.7 us for the VALU kernel with
+            // dynamic claims.
             if (stream_supported(a) && a.workers <= device_cus()) return SGD_KERNEL_STREAM;
             if (valu_supported(a)) return SGD_KERNEL_VALU;
             if (mfma_supported(a)) return SGD_KERNEL_MFMA;

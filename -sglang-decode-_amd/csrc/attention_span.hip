@@ -350,7 +350,7 @@ __device__ void merge_piece(SpanShared<NW> &sh, const sgd_decode_args &a0, int32
 }
 
 template <int DT, bool CSR, int NW, int DEPTH>
-__global__ __launch_bounds__(64 * NW, 2) void k_attention_span(sgd_decode_args a) {
+__global__ __launch_bounds__(64 * NW, NW > 4 ? 2 : 1) void k_attention_span(sgd_decode_args a) {
     extern __shared__ __align__(16) char dyn_smem[];
     SpanShared<NW> &sh = *reinterpret_cast<SpanShared<NW> *>(dyn_smem);
     const int lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
@@ -420,12 +420,13 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attention_span(sgd_decode_args a
         // ---- the pipeline's tile descriptors live in VGPR lanes: lane t % 8 of each ring
         // register holds tile t's field (tiles i .. i + 2 DEPTH - 1 are live), written by a
         // lane select and read with v_readlane, so no SGPRs carry them between stages.
-        static_assert(2 * DEPTH <= 8, "descriptor ring of 8 lanes");
+        constexpr int kRing = 2 * DEPTH <= 8 ? 8 : 16;
+        static_assert(2 * DEPTH <= kRing, "descriptor ring of 8 or 16 lanes");
         struct Ring {
             int32_t base, tok0, end, goff, qoff, slot, tl;
         } ring{};
         auto ring_put = [&](int32_t t, const Desc &d) {
-            const bool at = lane == (t & 7);
+            const bool at = lane == (t & (kRing - 1));
             ring.base = at ? d.base : ring.base;
             ring.tok0 = at ? d.tok0 : ring.tok0;
             ring.end = at ? d.end : ring.end;
@@ -434,7 +435,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attention_span(sgd_decode_args a
             ring.slot = at ? d.slot : ring.slot;
             ring.tl = at ? d.tl : ring.tl;
         };
-        auto ring_get = [&](int32_t field, int32_t t) { return __builtin_amdgcn_readlane(field, t & 7); };
+        auto ring_get = [&](int32_t field, int32_t t) { return __builtin_amdgcn_readlane(field, t & (kRing - 1)); };
 
         // ---- prologue.  Loads complete in issue order, so a wait for one load is a wait
         // for every older one: each tile's indices are issued before the K/V rows of the
@@ -509,11 +510,13 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attention_span(sgd_decode_args a
             // Two waves share a SIMD (slots v and v ^ 4) and the issue arbiter favours
             // the older one; the wave that is behind its partner takes the higher
             // priority, so the pair -- and the workgroup -- finish together.
-            if (lane == 0) __hip_atomic_store(&sh.prog[wave], i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            const int32_t partner = uni(__hip_atomic_load(&sh.prog[wave ^ 4], __ATOMIC_RELAXED,
-                                                          __HIP_MEMORY_SCOPE_WORKGROUP));
-            if (i <= partner) __builtin_amdgcn_s_setprio(2);
-            else __builtin_amdgcn_s_setprio(0);
+            if constexpr (NW == 8) {
+                if (lane == 0) __hip_atomic_store(&sh.prog[wave], i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                const int32_t partner = uni(__hip_atomic_load(&sh.prog[wave ^ 4], __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_WORKGROUP));
+                if (i <= partner) __builtin_amdgcn_s_setprio(2);
+                else __builtin_amdgcn_s_setprio(0);
+            }
             tile_compute<DT>(wt, sh.q[wave], nvalid, scale2, Roles(lane_v), m_l, den_l, acc);
             const bool task_end = d.tl == 0;
             if (task_end || i == count - 1) {

@@ -4,12 +4,16 @@ Workload (the headline configuration, `--workload c2`): batch 64, 32 q heads / 8
 heads, head_dim 128, bf16 KV ~ N(0,1), page_size 1 CSR token indices, contexts
 clip(round(exp(N(ln 1024, 0.8))), 128, 8192) (seeded), a 1M-token KV pool per layer
 with randomly permuted slots.  A step is one hipGraph replay of the plan build plus
-`--layers` layers (persistent attention, merge), each layer over its own KV pool so
-the working set exceeds the 256 MB Infinity Cache.  `--workload c3` is the skewed
-batch (2 x 32768 + 126 short requests, up to 64 splits), `--workload c4` the
-Llama-3-70B paged layer (page 16, 64 q / 8 kv, batch 32, contexts in [2048, 16384],
-200k-page pools; `--dtype fp16|bf16`), `--workload c5` the 32-layer step of the
-8B shape at batch 64 (contexts lognormal, median 2048).
+the model's layers (persistent attention, merge): 32 for the 8B shapes, 80 for
+Llama-3-70B (`--layers` overrides), so the plan -- built once per step and shared by
+every layer, as in a decode step -- is counted once per step.  The layers rotate
+over a few KV pools of their own (4 x 1M tokens = 16 GB for c2), so every layer's
+rows come from HBM: the working set far exceeds the 256 MB Infinity Cache.
+`--workload c3` is the skewed batch (2 x 32768 + 126 short requests, up to 64
+splits), `--workload c4` the Llama-3-70B paged layer (page 16, 64 q / 8 kv, batch
+32, contexts in [2048, 16384], 200k-page pools; `--dtype fp16|bf16`), `--workload
+c5` the 32-layer step of the 8B shape at batch 64 (contexts lognormal, median 2048)
+with a 256k-token pool per layer.
 
 Reported per schedule (R1, STATIC, STATIC_HOST, D1, D4, R0): us/layer = replay time /
 layers, achieved GB/s = algorithmic bytes per layer / us/layer.  STATIC builds its LPT
@@ -56,7 +60,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--layers", type=int, default=0, help="0 = 4 (c2, c3) or 2 (c4)")
+    ap.add_argument("--layers", type=int, default=0,
+                    help="layers per step; 0 = the model's: 32 (c2, c3, c5) or 80 (c4)")
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--dtype", default="bf16", choices=("bf16", "fp16"))
     ap.add_argument("--policies", default=",".join(POLICIES))
@@ -118,21 +123,26 @@ def main():
     lengths = W.lengths_for(args.workload)
     splits = W.split_hints(lengths, c.max_splits)
     batch = len(lengths)
-    layers = args.layers or {"c4": 2, "c5": 32}.get(args.workload, 4)
+    layers = args.layers or {"c4": 80}.get(args.workload, 32)
+    # distinct KV pools (and q, indices) the layers rotate over; each is used again only
+    # after the others' rows have streamed through the caches
+    pools = min(layers, {"c4": 2, "c5": 32}.get(args.workload, 4))
     csr = c.page_size == 1
     print(f"[bench] device={props.name} CUs={props.multi_processor_count} workers={workers} "
-          f"workload={args.workload} batch={batch} sumL={sum(lengths)} layers={layers}", flush=True)
+          f"workload={args.workload} batch={batch} sumL={sum(lengths)} layers={layers} pools={pools}", flush=True)
 
     if csr:
         pool_tokens = 1 << (18 if args.workload == "c5" else 20)
         fx = [W.make_csr_inputs(c, lengths, seed=1000 + i, device=dev, pool_tokens=pool_tokens, dtype=dtype,
-                                device_pool=True) for i in range(layers)]
+                                device_pool=True) for i in range(pools)]
+        fx = [fx[i % pools] for i in range(layers)]
         graph_kw = dict(indptrs=[x[4].numel() for x in fx])
         tables = [x[4] for x in fx]
         update_kw = dict(indptrs=[x[3] for x in fx])
     else:
         fx = [W.make_inputs(c, lengths, seed=1000 + i, device=dev, dtype=dtype, pool_pages=200_000,
-                            device_pool=True) for i in range(layers)]
+                            device_pool=True) for i in range(pools)]
+        fx = [fx[i % pools] for i in range(layers)]
         graph_kw = {}
         tables = [x[3][:batch] for x in fx]
         update_kw = {}
@@ -286,7 +296,7 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": args.dtype,
         "data": f"synthetic (seeded contexts, N(0,1) {args.dtype} q/K/V, randomly permuted KV pools)",
         "config": {"workload": WORKLOADS[args.workload], "name": args.workload,
-                   "batch": batch, "sum_context": sum(lengths), "layers_per_step": layers,
+                   "batch": batch, "sum_context": sum(lengths), "layers_per_step": layers, "kv_pools": pools,
                    "schedule": best, "workers": workers, "kernel": args.kernel,
                    "splits_total": sum(splits)},
         "us_per_layer": round(r["us_per_layer"], 2),

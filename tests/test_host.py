@@ -164,6 +164,24 @@ def test_struct_layouts_match_header(tmp_path):
             assert got[(cstruct, name)] == getattr(pystruct, name).offset, (cstruct, name)
 
 
+def test_span_constants_match_layout_header():
+    """The host sizes the span schedule's buffers with the kernel's constants
+    (csrc/span_layout.h): waves per workgroup (edge-state rows = span units / waves),
+    ints per wave record and floats per edge state."""
+    import re
+    from sglang_decode import config
+    text = open(os.path.join(ROOT, "-sglang-decode-_amd", "csrc", "span_layout.h")).read()
+    const = {m.group(1): int(m.group(2)) for m in re.finditer(r"constexpr int (k\w+) = (\d+);", text)}
+    assert config.SPAN_WAVES_PER_WORKGROUP == const["kWaves"]
+    assert config.span_workgroups(config.span_units("cpu")) * const["kWaves"] == config.span_units("cpu")
+    assert const["kRecord"] == 16  # runtime/workspace.py: span = ints(units * 16)
+    import torch
+    from sglang_decode.runtime.workspace import LayerBuffers
+    layer = LayerBuffers.allocate(config.DecodeConfig(), "cpu", torch.bfloat16)
+    assert tuple(layer.edge.shape) == (config.span_workgroups(config.span_units("cpu")), 2,
+                                       const["kHeads"] * const["kD"] + 2 * const["kHeads"])
+
+
 def test_host_static_lists_cpp_matches_reference(plan_vectors):
     from sglang_decode import _lib
     lib = _lib.lib()
