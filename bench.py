@@ -21,8 +21,9 @@ lists on the device inside the replay (the reference's device greedy, a serial
 chain); STATIC_HOST is the reference benchmark's host-static variant
 (benchmarks/bench_decode.py:14-30): C++ heap LPT on the host when the lengths change,
 lists installed after the device R1 plan.  `value` is the achieved HBM GB/s of the
-fastest schedule.  `roofline` times the attention kernel alone (HIP events on the
-launch stream around each launch, rotating layers) for that schedule.
+fastest schedule.  `roofline` times the attention kernel alone for that schedule: a
+HIP graph of back-to-back launches (rotating layers) replayed between HIP events on
+its stream.
 `cpu_baseline` is the FP32 oracle on the same inputs, timed on this host (bounded
 sample stated in the record).
 
@@ -231,18 +232,19 @@ def main():
             print("[bench] OUTPUT MISMATCH against the oracle", file=sys.stderr)
             sys.exit(3)
 
-    # roofline: attention kernel alone, HIP events on its launch stream, rotating layers
+    # roofline: the attention kernel alone, a batch of launches back to back (rotating
+    # layers) captured in a HIP graph and replayed between two HIP events on its stream,
+    # so no host work and no other kernel sits between launches (each launch returns its
+    # claim counter to zero when its last worker finishes).  The mean per launch over a
+    # replay; the median of 5 replays is reported.
     p = engine.plan
     stream = torch.cuda.current_stream(dev)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.kernel_launches)]
     engine.prepare()
-    for i in range(args.kernel_launches):
+
+    def launch(i):
         li = i % layers
         layer = engine.layers[li]
         x = fx[li]
-        layer.counter.zero_()
-        ev[i][0].record(stream)
         if csr:
             ks = (x[1].stride(0), 0, x[1].stride(1), x[1].stride(2))
             vs = (x[2].stride(0), 0, x[2].stride(1), x[2].stride(2))
@@ -251,10 +253,32 @@ def main():
             ks, vs, pts = x[1].stride(), x[2].stride(), graph.pages[li].stride()
         persistent_decode(p, layer, graph.q[li], x[1], x[2], graph.pages[li], graph.indptr[li],
                           c.head_dim ** -0.5, ks, vs, pts, csr, args.kernel)
-        ev[i][1].record(stream)
+
+    for layer in engine.layers:
+        layer.counter.zero_()
+    for i in range(layers):
+        launch(i)
     torch.cuda.synchronize()
-    durs = [a.elapsed_time(b) * 1000.0 for a, b in ev[len(ev) // 10:]]
-    kern_us = statistics.mean(durs)
+    batch_n = max(1, args.kernel_launches // 5)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(stream)
+    kgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(kgraph, stream=side):
+            for i in range(batch_n):
+                launch(i)
+    torch.cuda.synchronize()
+    kgraph.replay()
+    durs = []
+    for _ in range(5):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        kgraph.replay()
+        end.record(stream)
+        end.synchronize()
+        durs.append(start.elapsed_time(end) * 1000.0 / batch_n)
+    kern_us = statistics.median(durs)
     achieved = bytes_per_layer / (kern_us * 1e-6) / 1e9
     kernel_name = engine.attention_kernel_name()
     roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
