@@ -207,6 +207,23 @@ int sgd_merge_splits(const float *partial, const float *lse, const int32_t *coun
                      void *stream);
 
 /*
+ * Split merge after a span-schedule launch (SGD_KERNEL_SPAN); no reference
+ * counterpart (the reference runs every task whole in one program).  A task cut
+ * by a workgroup's range left unnormalized softmax states in `edge` (record 1 of
+ * the workgroup holding its first tile, record 0 of each later one); they are
+ * combined first and written to the task's (request, head, split) slot of
+ * partial / lse, so every slot holds its split's normalized partial and LSE as
+ * after sgd_merge_splits' inputs, then each row is merged as sgd_merge_splits
+ * does.  tile_prefix / chunk / edge / span_units are those of the launch;
+ * head_dim 128, group <= 4, partial and edge 16-byte aligned.
+ */
+int sgd_merge_splits_span(float *partial, float *lse, const int32_t *counts, const int32_t *error,
+                          void *out, const int32_t *tile_prefix, const int32_t *chunk,
+                          const float *edge, int32_t bcap, int32_t query_heads, int32_t kv_heads,
+                          int32_t head_dim, int32_t max_splits, int32_t span_units, int32_t dtype,
+                          void *stream);
+
+/*
  * Host (C++) LPT planner: heap assignment of planning/reference.py:57-67 over
  * host records, written as static lists the way benchmarks/bench_decode.py:14-30
  * uploads them.  All pointers are HOST pointers: weight[record_count],
