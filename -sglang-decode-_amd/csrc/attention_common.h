@@ -107,14 +107,27 @@ __device__ __forceinline__ Unit unit_of(const sgd_decode_args &a, int32_t u, int
     return r;
 }
 
-// Runs `run(task, info)` for every task of this worker, info being the task's record
-// (from the dispatch table for a unit's first task, else decode_task).  All threads of
-// the workgroup execute it uniformly; `sh_cursor` is one int of LDS.  In D1/D4 worker
-// w runs pack w first and its claims return workers + (counter): every pack still
-// runs exactly once.  The next unit is taken when the current one is done (a claim
-// made earlier, while a task streams, holds work back from workers that free up first
-// and measured slower).
-template <class Run>
+// A claim the run hook makes itself (for_each_task<true>): in D1/D4 the hook of a
+// unit's last task takes the next unit while its last tiles stream -- one relaxed
+// atomic on `counter` by one thread -- and stores base + (old value) to `slot` (the
+// worker's LDS cursor) before the workgroup barrier that ends its task.  slot is null
+// for the other tasks and in the other modes.
+struct Preclaim {
+    int32_t *slot;
+    int32_t *counter;
+    int32_t base;
+};
+
+// Runs `run(task, info)` (PRECLAIM: `run(task, info, preclaim)`) for every task of this
+// worker, info being the task's record (from the dispatch table for a unit's first
+// task, else decode_task).  All threads of the workgroup execute it uniformly;
+// `sh_cursor` is one int of LDS.  In D1/D4 worker w runs pack w first and its claims
+// return workers + (counter): every pack still runs exactly once.  Without PRECLAIM the
+// next unit is taken when the current one is done (a claim made while a task is still
+// streaming most of its tiles holds work back from workers that free up first, and
+// measured slower); with it, the hook claims during its last tile rounds, so the claim
+// round trip overlaps them and the unit waits one round at most.
+template <bool PRECLAIM = false, class Run>
 __device__ void for_each_task(const sgd_decode_args &a, int32_t *sh_cursor, Run &&run) {
     const int32_t worker = blockIdx.x;
     const int32_t mode = __builtin_amdgcn_readfirstlane(*a.mode);
@@ -146,9 +159,15 @@ __device__ void for_each_task(const sgd_decode_args &a, int32_t *sh_cursor, Run 
             ti.start = __builtin_amdgcn_readfirstlane(ti.start);
             ti.end = __builtin_amdgcn_readfirstlane(ti.end);
             ti.group = __builtin_amdgcn_readfirstlane(ti.group);
-            run(u.first + i, ti);
+            if constexpr (PRECLAIM)
+                run(u.first + i, ti, Preclaim{dynamic && i == u.count - 1 ? sh_cursor : nullptr, a.counter, claim_base});
+            else
+                run(u.first + i, ti);
         }
-        unit = dynamic ? claim() : mode == 2 ? __builtin_amdgcn_readfirstlane(a.static_next[unit]) : unit + a.workers;
+        if (dynamic && PRECLAIM)  // the hook stored it before its task's last barrier; the next
+            unit = __builtin_amdgcn_readfirstlane(*sh_cursor);  // store follows the next task's first
+        else
+            unit = dynamic ? claim() : mode == 2 ? __builtin_amdgcn_readfirstlane(a.static_next[unit]) : unit + a.workers;
     }
     // The last worker to finish puts the claim counter back to zero for the next
     // launch.  Relaxed is enough: a worker reaches this increment only after its

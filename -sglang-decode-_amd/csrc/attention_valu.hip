@@ -32,12 +32,15 @@ namespace {
 
 using namespace valu;
 
+constexpr int kIndptrLds = 256;  // CSR: kv_indptr entries kept in LDS (rows beyond read memory)
+
 template <int kWaves>
 struct ValuShared {
     WaveTile w[kWaves];
     uint4 q[kHeads][kD / 8];         // q rows of the current task
     float cm[kWaves][kHeads];
     float cd[kWaves][kHeads];
+    int32_t indptr[kIndptrLds];
     int32_t cursor;
 };
 
@@ -55,8 +58,16 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
     const float scale2 = a.scale * kLog2e;
     const int page_shift = __builtin_ctz((unsigned)a.page_size);  // page_size is a power of two here
     const int32_t page_mask = a.page_size - 1;
+    // CSR: kv_indptr (active + 1 entries) once per launch, so a task's index base is an
+    // LDS read rather than a memory round trip between its claim and its first loads.
+    int32_t iptr_n = 0;
+    if constexpr (CSR) {
+        iptr_n = min(__builtin_amdgcn_readfirstlane(*a.active) + 1, kIndptrLds);
+        for (int i = threadIdx.x; i < iptr_n; i += 64 * kWaves) sh.indptr[i] = a.indptr[i];
+        lds_barrier();
+    }
 
-    for_each_task(a, &sh.cursor, [&](int32_t, const TaskInfo &ti) {
+    for_each_task<true>(a, &sh.cursor, [&](int32_t, const TaskInfo &ti, const Preclaim &pc) {
         int lane = lane0;  // laundered per task: per-lane offsets are rebuilt, not held live
         asm volatile("" : "+v"(lane));
         // Global loads first -- q rows (wave 0), then the request's index base, the first
@@ -80,7 +91,7 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
         T.start = uni(ti.start);
         T.end = uni(ti.end);
         const int32_t split = uni(ti.split), group = uni(ti.group);
-        T.ind0 = CSR ? uni(a.indptr[T.request]) : 0;
+        T.ind0 = CSR ? uni(T.request < iptr_n ? sh.indptr[T.request] : a.indptr[T.request]) : 0;
         T.kbase = static_cast<const char *>(a.k) + group * (a.k_stride[2] * 2);
         T.vbase = static_cast<const char *>(a.v) + group * (a.v_stride[2] * 2);
         T.kp = a.k_stride[0] * 2;
@@ -121,7 +132,13 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
             tile_compute<DT>(wt, sh.q, nvalid, scale2, ro, m_l, den_l, acc);
         }
 
-        // ---- end of the wave's tiles: reduce within the wave, then merge the waves
+        // ---- end of the wave's tiles.  The last wave has the fewest tiles (round-robin
+        // deal): with none of its loads in flight, it takes the worker's next unit now, so
+        // the claim's round trip overlaps the other waves' last tiles; the merge barrier
+        // below publishes it to for_each_task.
+        if (pc.slot != nullptr && wave == kWaves - 1 && lane0 == 0)
+            *pc.slot = pc.base + __hip_atomic_fetch_add(pc.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // ---- reduce within the wave, then merge the waves
         const Roles ro(lane);
         float mh[kHeads], dh[kHeads];
         wave_state(m_l, den_l, acc, mh, dh);

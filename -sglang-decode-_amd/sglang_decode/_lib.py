@@ -57,6 +57,8 @@ _SIGNATURES = {
     "sgd_merge_splits": (_I, [_P] * 6 + [_I] * 5 + [_P]),
     "sgd_merge_splits_span": (_I, [_P] * 8 + [_I] * 7 + [_P]),
     "sgd_host_static_lists": (_I, [_P, _I, _I, _I, _I, _P, _P]),
+    "sgd_store_kv_stage_q": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, ctypes.c_int64, _P, _P, _P, _P,
+                                  _I, _I, _I, _I, _I, _P]),
 }
 
 _lib = None

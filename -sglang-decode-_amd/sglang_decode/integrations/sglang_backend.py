@@ -15,13 +15,15 @@ Environment: DECODE_DISABLE=1 keeps upstream decode; DECODE_MODE=AUTO|R0|R1|
 STATIC|D1|D4 forces a schedule; DECODE_POLICY=<validated policy json>;
 DECODE_BATCH_CAPACITY (default 64); DECODE_REUSE_PLAN=0 rebuilds the plan on
 every layer; DECODE_WORKERS overrides the persistent worker count (default: two
-per compute unit).
+per compute unit); DECODE_FUSED_KV=0 keeps upstream's set_kv_buffer and a separate
+q copy instead of the one-launch KV write + q staging (kernels/kv_store.py).
 """
 import os
 
 import torch
 
 from ..config import WORKGROUPS_PER_CU, DecodeConfig, Mode
+from ..kernels.kv_store import store_kv_and_stage_q
 from ..planning.policy import load_policy
 
 try:  # pragma: no cover - depends on an optional install
@@ -60,6 +62,11 @@ def layer_eligible(layer, config):
                 or getattr(layer, "sliding_window_size", -1) not in (None, -1))
 
 
+def _fused_device(t):
+    """The one-launch KV write + q staging runs on the GPU library."""
+    return t.device.type == "cuda"
+
+
 def make_backend_class(base):
     from ..runtime.engine import DecodeEngine
 
@@ -70,6 +77,7 @@ def make_backend_class(base):
             self._prepared = False
             self._eligible_step = False
             self.reuse_plan = os.getenv("DECODE_REUSE_PLAN", "1") == "1"
+            self.fused_kv = os.getenv("DECODE_FUSED_KV", "1") == "1"
             found = eligible_model(model_runner, self.num_head, self.num_kv_head)
             if found is None:
                 return
@@ -125,21 +133,33 @@ def make_backend_class(base):
             engine = self.scheduled
             if not self._eligible_step or not layer_eligible(layer, engine.config):
                 return super().forward_decode(q, k, v, layer, forward_batch, save_kv_cache)
-            if save_kv_cache:
-                forward_batch.token_to_kv_pool.set_kv_buffer(layer, forward_batch.out_cache_loc, k, v)
-            meta, p = self.forward_metadata, engine.plan
+            pool, c = forward_batch.token_to_kv_pool, engine.config
+            kbuf, vbuf = pool.get_key_buffer(layer.layer_id), pool.get_value_buffer(layer.layer_id)
             batch = q.shape[0]
+            fused = self.fused_kv and _fused_device(q)
+            k_new = v_new = None
+            if save_kv_cache:
+                if fused and k.dtype == kbuf.dtype and v.dtype == vbuf.dtype:
+                    # written by the launch below, together with the q staging (a pool
+                    # whose storage type differs from k's keeps upstream's conversion)
+                    k_new = k.view(batch, c.kv_heads, c.head_dim)
+                    v_new = v.view(batch, c.kv_heads, c.head_dim)
+                else:
+                    pool.set_kv_buffer(layer, forward_batch.out_cache_loc, k, v)
+            meta, p = self.forward_metadata, engine.plan
             if not self._prepared or not self.reuse_plan:
                 p.lengths[:batch].copy_(meta.kv_indptr[1:batch + 1] - meta.kv_indptr[:batch])
                 p.splits[:batch].copy_(meta.num_kv_splits[:batch])
                 engine.prepare()
                 self._prepared = True
             qbuf = self.query_buffers[layer.layer_id]
-            qbuf[:batch].copy_(q.view(batch, engine.config.query_heads, engine.config.head_dim))
-            out = engine.execute(
-                qbuf, forward_batch.token_to_kv_pool.get_key_buffer(layer.layer_id),
-                forward_batch.token_to_kv_pool.get_value_buffer(layer.layer_id), meta.kv_indices,
-                layer=layer.layer_id, indptr=meta.kv_indptr, scale=layer.scaling)
+            q_view = q.view(batch, c.query_heads, c.head_dim)
+            if fused:
+                store_kv_and_stage_q(k_new, v_new, forward_batch.out_cache_loc, kbuf, vbuf, q_view, qbuf)
+            else:
+                qbuf[:batch].copy_(q_view)
+            out = engine.execute(qbuf, kbuf, vbuf, meta.kv_indices, layer=layer.layer_id, indptr=meta.kv_indptr,
+                                 scale=layer.scaling)
             return out[:batch].view(batch, -1)
 
     return ScheduledTritonBackend

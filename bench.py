@@ -73,6 +73,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-check", action="store_true")
     ap.add_argument("--json-out", default="")
+    ap.add_argument("--kv-store", action="store_true",
+                    help="also time the decode step's KV-pool write + q staging: one launch "
+                         "(kernels/kv_store.py) against upstream's two scatters and a copy")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run a plain N-MiB read+write kernel 5 times, so a rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE pass can scale its counts to bytes")
@@ -96,6 +99,67 @@ def measured_traffic(path, kernel, workers, algorithmic_bytes):
                 kernel, workers, algorithmic_bytes):
             return row.get("traffic_bytes")
     return None
+
+
+def time_kv_store(c, fx, graph, batch, layers, csr, dtype, dev, reps=32, rounds=5):
+    """The decode step's KV-pool write + q staging for `batch` new tokens, per layer: one
+    launch of kernels/kv_store.py against what the reference adapter runs
+    (integrations/sglang_backend.py:91-92, 102-103: set_kv_buffer's two index_put
+    scatters, then qbuf[:batch].copy_).  Each captured in a HIP graph of `reps` layers
+    (rotating layers), replayed between HIP events; median of `rounds`.  Runs after the
+    measured steps: it overwrites `batch` slots of the pools."""
+    import torch
+    from sglang_decode.kernels.kv_store import store_kv_and_stage_q
+    g = torch.Generator(device=dev).manual_seed(99)
+    q = torch.randn((batch, c.query_heads, c.head_dim), generator=g, device=dev).to(dtype)
+    k = torch.randn((batch, c.kv_heads, c.head_dim), generator=g, device=dev).to(dtype)
+    v = torch.randn((batch, c.kv_heads, c.head_dim), generator=g, device=dev).to(dtype)
+    caches = []
+    for li in range(layers):
+        kc, vc = fx[li][1], fx[li][2]
+        if not csr:  # paged pools [pages, page, Hkv, D] hold tokens [pages * page, Hkv, D]
+            kc, vc = kc.view(-1, c.kv_heads, c.head_dim), vc.view(-1, c.kv_heads, c.head_dim)
+        caches.append((kc, vc))
+    tokens = caches[0][0].shape[0]
+    loc = torch.randperm(tokens, generator=torch.Generator().manual_seed(98))[:batch].to(dev)
+
+    def fused(i):
+        kc, vc = caches[i % layers]
+        store_kv_and_stage_q(k, v, loc, kc, vc, q, graph.q[i % layers])
+
+    def separate(i):
+        kc, vc = caches[i % layers]
+        kc[loc] = k
+        vc[loc] = v
+        graph.q[i % layers][:batch].copy_(q)
+
+    out = {}
+    for name, fn in (("fused_us", fused), ("separate_us", separate)):
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for i in range(3):
+                fn(i)
+        torch.cuda.synchronize()
+        cg = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(cg, stream=side):
+                for i in range(reps):
+                    fn(i)
+        torch.cuda.synchronize()
+        cg.replay()
+        durs = []
+        for _ in range(rounds):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record()
+            cg.replay()
+            b.record()
+            b.synchronize()
+            durs.append(a.elapsed_time(b) * 1000.0 / reps)
+        out[name] = round(statistics.median(durs), 2)
+    out["tokens"] = batch
+    return out
 
 
 def main():
@@ -289,6 +353,12 @@ def main():
                     algorithmic_bytes=bytes_per_layer)
     print(f"[bench] attention kernel alone ({best}): {kern_us:.2f} us  {achieved:.0f} GB/s", flush=True)
 
+    kv_store = None
+    if args.kv_store:
+        kv_store = time_kv_store(c, fx, graph, batch, layers, csr, dtype, dev)
+        print(f"[bench] kv write + q staging per layer: one launch {kv_store['fused_us']:.2f} us, "
+              f"upstream scatters + copy {kv_store['separate_us']:.2f} us", flush=True)
+
     if args.copy_calibration_mib:
         # a plain copy kernel of known size: N MiB read + N MiB written per launch
         n = args.copy_calibration_mib * (1 << 20) // 2
@@ -333,6 +403,8 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
+    if kv_store is not None:
+        line["kv_store"] = kv_store
     text = json.dumps(line)
     if args.json_out:
         with open(args.json_out, "w") as f:

@@ -224,6 +224,26 @@ int sgd_merge_splits_span(float *partial, float *lse, const int32_t *counts, con
                           void *stream);
 
 /*
+ * The decode step's writes around the attention, one launch per layer.  Replaces the
+ * reference adapter's token_to_kv_pool.set_kv_buffer(layer, out_cache_loc, k, v)
+ * (integrations/sglang_backend.py:91-92; upstream two scatters) and
+ * qbuf[:batch].copy_(q.view(batch, Hq, D)) (:102-103).  For b < batch:
+ *   k_cache[loc[b]] = k_new[b], v_cache[loc[b]] = v_new[b]   ([Hkv, D] rows)
+ *   q_out[b] = q_in[b]                                       ([Hq, D] rows)
+ * bit for bit (no conversion; 16-bit dtype).  Either part may be skipped: k_new NULL
+ * (save_kv_cache off) or q_in NULL.  Strides are element strides of dims 0 and 1 (dim 2
+ * has unit stride): new_strides {k0, k1, v0, v1}, cache_strides {k0, k1, v0, v1},
+ * q_in_strides / q_out_strides {0, 1}; all multiples of 8 elements and every base
+ * 16-byte aligned.  loc is int32, or int64 when loc_is_int64; a slot outside
+ * [0, cache_tokens) is skipped on the device.  Returns SGD_EINVAL for misuse.
+ */
+int sgd_store_kv_stage_q(const void *k_new, const void *v_new, const int64_t *new_strides, const void *loc,
+                         int32_t loc_is_int64, void *k_cache, void *v_cache, const int64_t *cache_strides,
+                         int64_t cache_tokens, const void *q_in, const int64_t *q_in_strides, void *q_out,
+                         const int64_t *q_out_strides, int32_t batch, int32_t kv_heads, int32_t query_heads,
+                         int32_t head_dim, int32_t dtype, void *stream);
+
+/*
  * Host (C++) LPT planner: heap assignment of planning/reference.py:57-67 over
  * host records, written as static lists the way benchmarks/bench_decode.py:14-30
  * uploads them.  All pointers are HOST pointers: weight[record_count],

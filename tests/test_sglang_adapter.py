@@ -89,7 +89,7 @@ def layer(layer_id, heads=32, kv_heads=8, head_dim=128, **kw):
 @pytest.fixture(autouse=True)
 def clean_env(monkeypatch):
     for name in ("DECODE_DISABLE", "DECODE_MODE", "DECODE_POLICY", "DECODE_BATCH_CAPACITY",
-                 "DECODE_REUSE_PLAN", "DECODE_WORKERS"):
+                 "DECODE_REUSE_PLAN", "DECODE_WORKERS", "DECODE_FUSED_KV"):
         monkeypatch.delenv(name, raising=False)
 
 
@@ -180,6 +180,59 @@ def test_decode_step_data_flow_and_plan_reuse(monkeypatch, reuse):
     assert torch.equal(e["q"][:3], q.view(3, 32, 128))  # per-layer q buffer at capture capacity
     assert e["q"].shape == (64, 32, 128)
     assert b.mr_pool.writes == [0, 1]
+
+
+class StoreRecorder:
+    """Stands in for the one-launch KV write + q staging on a CPU-only host."""
+
+    def __init__(self):
+        self.calls = []
+
+    def __call__(self, k_new, v_new, loc, k_cache, v_cache, q_in, q_out):
+        self.calls.append(dict(k_new=k_new, v_new=v_new, loc=loc, k_cache=k_cache, v_cache=v_cache, q_in=q_in,
+                               q_out=q_out))
+        q_out[:q_in.shape[0]].copy_(q_in)
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float32])
+def test_fused_kv_write_and_q_staging(monkeypatch, kv_dtype):
+    """On the GPU the adapter replaces set_kv_buffer and the q copy with one launch
+    (kernels/kv_store.py); a k/v dtype other than the pool's keeps set_kv_buffer (its
+    conversion) while q is still staged by the launch."""
+    from sglang_decode.integrations import sglang_backend as SB
+    store = StoreRecorder()
+    monkeypatch.setattr(SB, "store_kv_and_stage_q", store)
+    monkeypatch.setattr(SB, "_fused_device", lambda t: True)
+    b = make_backend()
+    rec = Recorder(b.scheduled)
+    fb = decode_batch(b, [5, 17, 3], [1, 2, 1])
+    fb.out_cache_loc = torch.tensor([4, 21, 24], dtype=torch.int64)
+    b.init_forward_metadata(fb)
+    q = torch.randn(3, 32 * 128).to(torch.bfloat16)
+    kv = torch.randn(3, 8 * 128).to(kv_dtype)
+    for lid in range(2):
+        b.forward_decode(q, kv, kv, layer(lid), fb, save_kv_cache=True)
+    assert [e["layer"] for e in rec.executes] == [0, 1]
+    assert len(store.calls) == 2
+    for lid, call in enumerate(store.calls):
+        assert call["q_out"] is b.query_buffers[lid] and call["k_cache"] is b.mr_pool.keys[lid]
+        assert call["v_cache"] is b.mr_pool.values[lid] and call["loc"] is fb.out_cache_loc
+        assert torch.equal(call["q_in"], q.view(3, 32, 128))
+        assert rec.executes[lid]["k"] is b.mr_pool.keys[lid]
+        if kv_dtype == torch.bfloat16:
+            assert call["k_new"].shape == (3, 8, 128) and torch.equal(call["k_new"], kv.view(3, 8, 128))
+        else:
+            assert call["k_new"] is None and call["v_new"] is None
+    assert b.mr_pool.writes == ([] if kv_dtype == torch.bfloat16 else [0, 1])
+    # DECODE_FUSED_KV=0: upstream set_kv_buffer and a separate q copy
+    monkeypatch.setenv("DECODE_FUSED_KV", "0")
+    b = make_backend()
+    Recorder(b.scheduled)
+    fb = decode_batch(b, [5, 17, 3], [1, 2, 1])
+    b.init_forward_metadata(fb)
+    store.calls.clear()
+    b.forward_decode(q, kv, kv, layer(0), fb, save_kv_cache=True)
+    assert store.calls == [] and b.mr_pool.writes == [0]
 
 
 def test_step_and_layer_gates_fall_back_to_upstream():
