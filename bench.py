@@ -24,6 +24,9 @@ lists installed after the device R1 plan.  `value` is the achieved HBM GB/s of t
 fastest schedule.  `roofline` times the attention kernel alone for that schedule: a
 HIP graph of back-to-back launches (rotating layers) replayed between HIP events on
 its stream.
+`attention_merge_us` (attention + merge per layer, no plan) and `single_layer_entry_us`
+(one layer's full entry: plan build + attention + merge, the reference's
+benchmarks/bench_decode.py:94 boundary) are timed the same way for that schedule.
 `cpu_baseline` is the FP32 oracle on the same inputs, timed on this host (bounded
 sample stated in the record).
 
@@ -101,6 +104,35 @@ def measured_traffic(path, kernel, workers, algorithmic_bytes):
     return None
 
 
+def graph_time(fn, reps, dev, rounds=5):
+    """Median per-call time (us) of fn(0) .. fn(reps - 1) captured in one HIP graph and
+    replayed between HIP events on the current stream."""
+    import torch
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for i in range(min(reps, 3)):
+            fn(i)
+    torch.cuda.synchronize()
+    cg = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(cg, stream=side):
+            for i in range(reps):
+                fn(i)
+    torch.cuda.synchronize()
+    cg.replay()
+    durs = []
+    for _ in range(rounds):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        cg.replay()
+        b.record()
+        b.synchronize()
+        durs.append(a.elapsed_time(b) * 1000.0 / reps)
+    return statistics.median(durs)
+
+
 def time_kv_store(c, fx, graph, batch, layers, csr, dtype, dev, reps=32, rounds=5):
     """The decode step's KV-pool write + q staging for `batch` new tokens, per layer: one
     launch of kernels/kv_store.py against what the reference adapter runs
@@ -133,31 +165,8 @@ def time_kv_store(c, fx, graph, batch, layers, csr, dtype, dev, reps=32, rounds=
         vc[loc] = v
         graph.q[i % layers][:batch].copy_(q)
 
-    out = {}
-    for name, fn in (("fused_us", fused), ("separate_us", separate)):
-        side = torch.cuda.Stream(dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side):
-            for i in range(3):
-                fn(i)
-        torch.cuda.synchronize()
-        cg = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(cg, stream=side):
-                for i in range(reps):
-                    fn(i)
-        torch.cuda.synchronize()
-        cg.replay()
-        durs = []
-        for _ in range(rounds):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            a.record()
-            cg.replay()
-            b.record()
-            b.synchronize()
-            durs.append(a.elapsed_time(b) * 1000.0 / reps)
-        out[name] = round(statistics.median(durs), 2)
+    out = {name: round(graph_time(fn, reps, dev, rounds), 2) for name, fn in (("fused_us", fused),
+                                                                              ("separate_us", separate))}
     out["tokens"] = batch
     return out
 
@@ -353,6 +362,22 @@ def main():
                     algorithmic_bytes=bytes_per_layer)
     print(f"[bench] attention kernel alone ({best}): {kern_us:.2f} us  {achieved:.0f} GB/s", flush=True)
 
+    # the reference's other boundaries (benchmarks/bench_decode.py:94): one layer's full
+    # entry (plan build + attention + merge) and attention + merge without the plan, per
+    # layer, for the reported schedule
+    def layer_call(i):
+        li = i % layers
+        engine.execute(graph.q[li], *graph.kv_pairs[li], graph.pages[li], layer=li, indptr=graph.indptr[li])
+
+    def full_entry(i):
+        engine.prepare()
+        layer_call(0)
+
+    attn_merge_us = graph_time(layer_call, layers, dev)
+    single_layer_us = graph_time(full_entry, 8, dev)
+    print(f"[bench] attention + merge ({best}): {attn_merge_us:.2f} us/layer; single-layer full entry "
+          f"(plan + attention + merge): {single_layer_us:.2f} us", flush=True)
+
     kv_store = None
     if args.kv_store:
         kv_store = time_kv_store(c, fx, graph, batch, layers, csr, dtype, dev)
@@ -402,6 +427,8 @@ def main():
         "check": check,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "attention_merge_us": round(attn_merge_us, 2),
+        "single_layer_entry_us": round(single_layer_us, 2),
     }
     if kv_store is not None:
         line["kv_store"] = kv_store
