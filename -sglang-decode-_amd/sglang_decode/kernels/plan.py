@@ -50,8 +50,9 @@ def greedy_lists(plan):
         "greedy_lists")
 
 
-def fused_build(plan, force_mode=-1, run_greedy=False, counters=None):
-    """All stages in one launch; optionally clears ``counters`` (int32) in the same launch."""
+def fused_build(plan, force_mode=-1, run_greedy=False, counters=None, spans=True):
+    """All stages in one launch; optionally clears ``counters`` (int32) in the same launch;
+    ``spans`` also writes the span schedule's tables."""
     n = 0 if counters is None else counters.numel()
-    check(_lib.lib().sgd_build_plan(ctypes.byref(plan.c_struct()), int(force_mode), int(bool(run_greedy)),
+    check(_lib.lib().sgd_build_plan(ctypes.byref(plan.c_struct(spans)), int(force_mode), int(bool(run_greedy)),
                                     ptr(counters), n, _s(plan)), "build_plan")

@@ -13,12 +13,15 @@ results; used by the parity tests of each stage).
 from ..kernels import plan as K
 
 
-def build_plan(plan, force_mode=-1, *, fused=True, counters=None):
+def build_plan(plan, force_mode=-1, *, fused=True, counters=None, spans=False):
+    """``spans``: the fused build also writes the span schedule's tables (only the span
+    kernel reads them)."""
     force_mode = int(force_mode)
     run_greedy = force_mode == 2 or any_static_rule(plan)
     if fused:
-        K.fused_build(plan, force_mode, run_greedy, counters)
-        plan.dispatch_valid = plan.span_valid = True
+        K.fused_build(plan, force_mode, run_greedy, counters, spans)
+        plan.dispatch_valid = True
+        plan.span_valid = bool(spans)
         return
     plan.dispatch_valid = plan.span_valid = False  # the stage launches write neither table
     if counters is not None:

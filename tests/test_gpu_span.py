@@ -51,7 +51,7 @@ def csr_case(c, lengths, seed, splits=None, mode=Mode.R1, dtype=torch.bfloat16):
 def test_span_tables_match_oracle(mode, lengths, splits):
     c = DecodeConfig(batch_capacity=8, max_context=4096, page_size=1)
     splits = splits or W.split_hints(lengths, c.max_splits)
-    engine = DecodeEngine(c, force_mode=mode)
+    engine = DecodeEngine(c, force_mode=mode, kernel="span")
     W.update_plan(engine, lengths, splits)
     engine.prepare()
     torch.cuda.synchronize()
