@@ -366,18 +366,18 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
         }
         lds_barrier();
     }
-    // Pack tables, one sorted record position per thread: its tasks that start a pack.
+    // Pack tables, one task per thread (consecutive threads, consecutive tasks: the
+    // stores of a wave land on neighbouring pack entries, not one record's Hkv tasks
+    // per lane): a task that starts a pack writes it.
     const BucketRegs R(sh, lane);
-    for (int j = tid; j < total; j += kPlanThreads) {
-        const BucketOf o = bucket_at(R, j, buckets);
-        for (int g = 0; g < hkv; ++g) {
-            int32_t count;
-            const int32_t task = j * hkv + g;
-            const int32_t unit = pack_of(o, task, hkv, count);
-            if (unit >= 0) {
-                pack_first[unit] = task;
-                pack_count[unit] = count;
-            }
+    const int32_t ntasks = wmul(total, hkv);
+    for (int32_t task = tid; task < ntasks; task += kPlanThreads) {
+        const BucketOf o = bucket_at(R, task / hkv, buckets);
+        int32_t count;
+        const int32_t unit = pack_of(o, task, hkv, count);
+        if (unit >= 0) {
+            pack_first[unit] = task;
+            pack_count[unit] = count;
         }
     }
 }
@@ -484,24 +484,23 @@ __device__ void stage_dispatch_table(int32_t *table, int32_t capacity, const int
     const int32_t mode = sh.mode;
     if (mode == 0) return;
     const BucketRegs R(sh, threadIdx.x & 63);
-    // one record per thread: its request found once, then its Hkv tasks
-    for (int32_t j = threadIdx.x; j < total; j += kPlanThreads) {
+    // one task per thread, so a wave writes neighbouring entries (the Hkv lanes of a
+    // record find its request together: their LDS reads are broadcasts)
+    const int32_t ntasks = wmul(total, hkv);
+    for (int32_t task = threadIdx.x; task < ntasks; task += kPlanThreads) {
+        const int32_t j = task / hkv, g = task - j * hkv;
         const int32_t rec = mode >= 3 ? (int32_t)order_mirror[j] : j;
         const int32_t r = request_of(rows.offsets, bcap, rec);
         const int32_t s = wadd(rec, -rows.offsets[r]);
         const int32_t c = rows.chunk[r];
         const int32_t b = wmul(s, c);
         const int32_t e = min(wadd(b, c), rows.lengths[r]);
-        const BucketOf o = bucket_at(R, j, buckets);
-        for (int32_t g = 0; g < hkv; ++g) {
-            const int32_t task = j * hkv + g;
-            int32_t count = 1, unit = task;
-            if (mode >= 3) unit = pack_of(o, task, hkv, count);
-            if (unit < 0 || unit >= capacity) continue;
-            int32_t *ent = table + 8 * (int64_t)unit;
-            *reinterpret_cast<int4 *>(ent) = make_int4(task, count, r, s);
-            *reinterpret_cast<int4 *>(ent + 4) = make_int4(b, e, g, mode >= 3 ? 2 : 1);
-        }
+        int32_t count = 1, unit = task;
+        if (mode >= 3) unit = pack_of(bucket_at(R, j, buckets), task, hkv, count);
+        if (unit < 0 || unit >= capacity) continue;
+        int32_t *ent = table + 8 * (int64_t)unit;
+        *reinterpret_cast<int4 *>(ent) = make_int4(task, count, r, s);
+        *reinterpret_cast<int4 *>(ent + 4) = make_int4(b, e, g, mode >= 3 ? 2 : 1);
     }
 }
 
