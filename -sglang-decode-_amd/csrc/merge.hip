@@ -1,22 +1,22 @@
 // Split merge: per (request, query head), LSE-weighted combination of the
 // normalized partial outputs of its splits (kernels/merge.py:7-30).
 //
-// One wave per (request, head).  The merge is latency-bound (a few KB per row),
-// so the dependent chain is two memory round trips: the split count, then the
-// split LSEs (one per lane) together with up to kRowsInFlight partial rows
-// (each a coalesced 256-1024 B burst, lanes owning head_dim/64 consecutive dims),
-// all issued before any is used.  The global max and the weights exp(lse_s - max)
-// come from wave reductions.  This is the two-pass form of the reference's
-// running-max merge (same value up to rounding).  Rows with no split produce
-// exact zeros (0 / max(den, 1e-30)); a plan error produces NaN.
+// The merge is latency-bound (a few KB per row): the split count, then the split
+// LSEs together with up to kRowsInFlight partial rows (each a coalesced 256-1024 B
+// burst, lanes owning head_dim/64 consecutive dims), all issued before any is used.
+// A row with more splits is cut over the workgroup's waves (k_merge).  The max and
+// the weights exp(lse_s - max) come from wave reductions, combined online from block
+// to block and wave to wave in a fixed order: the value of the reference's running-max
+// merge up to rounding.  Rows with no split produce exact zeros (0 / max(den, 1e-30));
+// a plan error produces NaN.
 #include "common.h"
 #include "span_layout.h"
 
 namespace sgd {
 namespace {
 
-constexpr int kMergeWaves = 4;
-constexpr int kRowsInFlight = 16;  // divides 64: a block of rows never straddles two LSE blocks
+constexpr int kMergeWaves = 1;  // span merge: one (request, head) per workgroup
+constexpr int kRowsInFlight = 16;  // split rows (and the span merge's edge rows) per round trip
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <int DPL>
@@ -32,67 +32,122 @@ __device__ __forceinline__ void load_row(const float *src, float (&v)[DPL]) {
     }
 }
 
-// The merge of one (request, head) row by one wave: n splits of partial/lse rows at
-// prow / lrow (row `row` of out).
-template <int DT, int DPL>  // DPL = dims per lane
-__device__ __forceinline__ void merge_row(const float *__restrict__ partial, const float *__restrict__ lse,
-                                          int32_t n, bool bad, uint16_t *__restrict__ out, int64_t row,
-                                          int32_t smax, int lane) {
+// One wave's LSE-weighted sum over splits [s0, s1) of the (request, head) row `row`:
+// its running max m (log2 domain), denominator and unnormalized sum acc (this lane's
+// DPL dims), built in blocks of kRowsInFlight split rows -- each block's rows and
+// LSEs in flight together -- combined online from block to block.  An empty range
+// leaves (-inf, 0, 0).
+template <int DPL>
+__device__ __forceinline__ void merge_part(const float *__restrict__ partial, const float *__restrict__ lse,
+                                           int64_t row, int32_t smax, int32_t s0, int32_t s1, int lane,
+                                           float &m, float &den, float (&acc)[DPL]) {
     constexpr int D = DPL * 64;
     const float *lrow = lse + row * smax;
     const float *prow = partial + row * smax * D + lane * DPL;
-    float den = 0.f, acc[DPL];
+    m = -INFINITY;
+    den = 0.f;
 #pragma unroll
     for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
-    float mx = -INFINITY;
-    if (n > 64) {  // more splits than lanes: the max first, over all of them
-        for (int b = 0; b < n; b += 64)
-            mx = fmaxf(mx, wave_max(b + lane < n ? lrow[b + lane] * kLog2e : -INFINITY));
-    }
-    for (int b = 0; b < n; b += kRowsInFlight) {
-        // rows b .. b+kRowsInFlight-1 and (per 64 rows) their LSEs, all in flight at once
+    for (int b = s0; b < s1; b += kRowsInFlight) {
         float v[kRowsInFlight][DPL];
 #pragma unroll
         for (int s = 0; s < kRowsInFlight; ++s) {
-            if (b + s < n) load_row<DPL>(prow + (int64_t)(b + s) * D, v[s]);
+            if (b + s < s1) load_row<DPL>(prow + (int64_t)(b + s) * D, v[s]);
             else
 #pragma unroll
                 for (int i = 0; i < DPL; ++i) v[s][i] = 0.f;
         }
-        const int lb = b & ~63;  // LSE block holding rows b..: lane l has split lb + l
-        const float l2 = lb + lane < n ? lrow[lb + lane] * kLog2e : -INFINITY;
-        if (n <= 64 && b == 0) mx = wave_max(l2);
-        const float w = lb + lane < n ? __builtin_amdgcn_exp2f(l2 - mx) : 0.f;
-        if ((b & 63) == 0) den += wave_sum(w);
+        // lane l < kRowsInFlight holds split b + l's LSE
+        const bool mine = lane < kRowsInFlight && b + lane < s1;
+        const float l2 = mine ? lrow[b + lane] * kLog2e : -INFINITY;
+        const float mb = fmaxf(m, wave_max(l2));
+        const float so = __builtin_amdgcn_exp2f(m - mb);  // 0 for the first block (m = -inf)
+        const float w = mine ? __builtin_amdgcn_exp2f(l2 - mb) : 0.f;
+        den = den * so + wave_sum(w);
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc[i] *= so;
 #pragma unroll
         for (int s = 0; s < kRowsInFlight; ++s) {
-            if (b + s < n) {
-                const float ws = __builtin_bit_cast(
-                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), (b + s - lb)));
+            if (b + s < s1) {
+                const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
 #pragma unroll
                 for (int i = 0; i < DPL; ++i) acc[i] += v[s][i] * ws;
             }
         }
+        m = mb;
     }
+}
+
+// The merged row out = acc / den (0 for a row without splits, NaN on a plan error).
+template <int DT, int DPL>
+__device__ __forceinline__ void store_row(uint16_t *__restrict__ out, int64_t row, float den,
+                                          const float (&acc)[DPL], bool bad, int lane) {
     const float inv = 1.0f / fmaxf(den, 1.0e-30f);
-    uint16_t *dst = out + row * D + lane * DPL;
+    uint16_t *dst = out + row * (DPL * 64) + lane * DPL;
 #pragma unroll
     for (int i = 0; i < DPL; ++i) dst[i] = (uint16_t)from_f32<DT>(bad ? __builtin_nanf("") : acc[i] * inv);
 }
 
+// The merge of one (request, head) row by one wave: n splits of partial/lse rows.
+template <int DT, int DPL>  // DPL = dims per lane
+__device__ __forceinline__ void merge_row(const float *__restrict__ partial, const float *__restrict__ lse,
+                                          int32_t n, bool bad, uint16_t *__restrict__ out, int64_t row,
+                                          int32_t smax, int lane) {
+    float m, den, acc[DPL];
+    merge_part<DPL>(partial, lse, row, smax, 0, n, lane, m, den, acc);
+    store_row<DT, DPL>(out, row, den, acc, bad, lane);
+}
+
+// One workgroup of kSplitWaves waves per (request, head).  A row with at most
+// kRowsInFlight splits is merged by wave 0 alone (one round trip for its data); a
+// longer one is cut into kSplitWaves contiguous split ranges, merged by the waves side
+// by side and combined in wave order through LDS -- so a 64-split row costs a block's
+// round trip, not four.
+constexpr int kSplitWaves = 4;
+
 template <int DT, int DPL>
-__global__ __launch_bounds__(64 * kMergeWaves) void k_merge(const float *__restrict__ partial,
+__global__ __launch_bounds__(64 * kSplitWaves) void k_merge(const float *__restrict__ partial,
                                                             const float *__restrict__ lse,
                                                             const int32_t *__restrict__ counts,
                                                             const int32_t *__restrict__ error,
                                                             uint16_t *__restrict__ out, int32_t hq,
                                                             int32_t smax) {
-    const int lane = threadIdx.x & 63;
-    const int head = blockIdx.y * kMergeWaves + (threadIdx.x >> 6);
-    const int r = blockIdx.x;
-    if (head >= hq) return;
+    __shared__ float sm[kSplitWaves], sd[kSplitWaves], sacc[kSplitWaves][DPL * 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = blockIdx.x, head = blockIdx.y;
     const int32_t n = __builtin_amdgcn_readfirstlane(counts[r]);
-    merge_row<DT, DPL>(partial, lse, n, *error != 0, out, (int64_t)r * hq + head, smax, lane);
+    const bool bad = *error != 0;
+    const int64_t row = (int64_t)r * hq + head;
+    if (n <= kRowsInFlight) {
+        if (wave == 0) merge_row<DT, DPL>(partial, lse, n, bad, out, row, smax, lane);
+        return;  // n is the workgroup's: no wave waits below
+    }
+    const int32_t q = (n + kSplitWaves - 1) / kSplitWaves;
+    float m, den, acc[DPL];
+    merge_part<DPL>(partial, lse, row, smax, min(wave * q, n), min((wave + 1) * q, n), lane, m, den, acc);
+    if (lane == 0) {
+        sm[wave] = m;
+        sd[wave] = den;
+    }
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) sacc[wave][lane * DPL + i] = acc[i];
+    lds_barrier();
+    if (wave != 0) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kSplitWaves; ++k) M = fmaxf(M, sm[k]);
+    float D = 0.f, X[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) X[i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < kSplitWaves; ++k) {
+        if (sd[k] == 0.f) continue;  // an empty range
+        const float sc = __builtin_amdgcn_exp2f(sm[k] - M);
+        D += sd[k] * sc;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) X[i] += sacc[k][lane * DPL + i] * sc;
+    }
+    store_row<DT, DPL>(out, row, D, X, bad, lane);
 }
 
 // The common case of the span merge in two memory round trips: the row's split
@@ -294,8 +349,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge_span(
 template <int DT>
 int launch_merge(const float *partial, const float *lse, const int32_t *counts, const int32_t *error, void *out,
                  int32_t bcap, int32_t hq, int32_t d, int32_t smax, hipStream_t stream) {
-    const dim3 grid(bcap, (hq + kMergeWaves - 1) / kMergeWaves);
-    const dim3 block(64 * kMergeWaves);
+    const dim3 grid(bcap, hq), block(64 * kSplitWaves);
     auto *o = static_cast<uint16_t *>(out);
     switch (d) {
         case 64: hipLaunchKernelGGL((k_merge<DT, 1>), grid, block, 0, stream, partial, lse, counts, error, o, hq, smax); break;

@@ -213,3 +213,25 @@ def test_llama70b_paged_shape_subset(dtype):
     engine = DecodeEngine(c, dtype=dtype, force_mode=Mode.D1)
     out = run(engine, lengths, inputs)
     close(out[:6], OA.paged_attention(*inputs[:3], inputs[3], lengths, c.page_size))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("csr", [False, True])
+def test_rows_with_many_splits(csr, dtype):
+    """Rows of 17, 40 and 64 splits (merged by several waves of one workgroup, split
+    ranges combined in a fixed order) beside rows of 1-16 splits and an empty row."""
+    c = DecodeConfig(batch_capacity=8, max_splits=64, max_context=8192, page_size=1 if csr else 16, workers=64)
+    lengths = [8192, 1, 2100, 0, 5000, 700, 64 * 32 + 5, 300]
+    splits = [64, 1, 17, 1, 40, 16, 64, 3]
+    if csr:
+        q, k, v, indptr, indices = W.make_csr_inputs(c, lengths, seed=31, dtype=dtype, pool_tokens=1 << 15)
+        inputs, exp = (q, k, v, indices), OA.csr_attention(q, k, v, indptr, indices, lengths)
+    else:
+        inputs, indptr = W.make_inputs(c, lengths, seed=31, dtype=dtype), None
+        exp = OA.paged_attention(*inputs[:3], inputs[3], lengths, c.page_size)
+    engine = DecodeEngine(c, dtype=dtype, force_mode=Mode.D1)
+    out = run(engine, lengths, inputs, indptr=indptr, splits=splits)
+    counts = engine.plan.counts[:len(lengths)].tolist()
+    assert max(counts) == 64 and sum(n > 16 for n in counts) == 4  # the multi-wave path runs
+    close(out[:len(lengths)], exp[:len(lengths)])
+    assert not out[len(lengths):].float().abs().sum().item()
