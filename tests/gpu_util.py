@@ -45,7 +45,7 @@ def assert_plan_equal(dev, ref, config, active, name=""):
             OP.walk_lists(ref["static_head"], ref["static_next"]), name
 
 
-def close(actual, expected, atol=2e-2, rtol=1e-2):
+def close(actual, expected, atol=2e-2, rtol=1e-2, msg=""):
     """The path's tolerance for bf16/fp16 inputs vs the FP32 oracle: 2e-2 abs / 1e-2 rel."""
     a = actual.float().cpu().numpy() if isinstance(actual, torch.Tensor) else np.asarray(actual)
-    np.testing.assert_allclose(a, expected, atol=atol, rtol=rtol)
+    np.testing.assert_allclose(a, expected, atol=atol, rtol=rtol, err_msg=msg)
