@@ -53,13 +53,25 @@ struct RowMirror {
 
 constexpr int kMaxRowsPerThread = 4;  // bcap <= 4096 = 4 x kPlanThreads
 
+// The plan's inputs taken from the CSR metadata of the step instead of the plan's own
+// lengths/splits/active buffers: rows r < batch get length kv_indptr[r+1] - kv_indptr[r]
+// and split count num_kv_splits[r], active = batch -- the values the reference adapter
+// copies into the plan before every build (integrations/sglang_backend.py:98-99) -- and
+// those values are also stored to the plan's buffers (the attention reads them).
+struct CsrRows {
+    const int32_t *indptr, *splits;
+    int32_t batch;
+    int32_t *lengths_out, *splits_out, *active_out;
+};
+
 __device__ void stage_count_scan(const int32_t *lengths, const int32_t *splits, const int32_t *active_p,
                                  int32_t *counts, int32_t *offsets, int32_t *chunk, int32_t *record_count,
                                  int32_t *error, int32_t bcap, int32_t smax, int32_t max_context,
-                                 PlanShared &sh, const RowMirror *mirror = nullptr) {
+                                 PlanShared &sh, const RowMirror *mirror = nullptr, const CsrRows *csr = nullptr) {
     const int tid = threadIdx.x;
     const int per = (bcap + kPlanThreads - 1) / kPlanThreads;  // rows per thread (contiguous)
-    const int32_t active = *active_p;
+    const int32_t active = csr ? csr->batch : *active_p;
+    if (csr && tid == 0) *csr->active_out = active;
     const int r0 = tid * per;
     int invalid_any = 0;
     int32_t local = 0, nrow[kMaxRowsPerThread];
@@ -70,7 +82,18 @@ __device__ void stage_count_scan(const int32_t *lengths, const int32_t *splits, 
         const int r = r0 + i;
         if (i >= per || r >= bcap) continue;
         const bool live = r < active;
-        const int32_t raw_length = lengths[r], raw_split = splits[r];  // issued with the load of active
+        int32_t raw_length, raw_split;  // issued with the load of active
+        if (csr) {
+            raw_length = live ? wadd(csr->indptr[r + 1], -csr->indptr[r]) : 0;
+            raw_split = live ? csr->splits[r] : 1;
+            if (live) {
+                csr->lengths_out[r] = raw_length;
+                csr->splits_out[r] = raw_split;
+            }
+        } else {
+            raw_length = lengths[r];
+            raw_split = splits[r];
+        }
         const int32_t length = live ? raw_length : 0;
         const int32_t s = live ? raw_split : 1;
         const bool invalid = live && (length < 0 || length > max_context || s < 1 || s > smax);
@@ -663,7 +686,9 @@ static_assert(sizeof(FusedLds) <= 160 * 1024, "fused plan LDS");
 // All stages in one launch; every intermediate that a later stage reads stays in LDS,
 // so the stages wait on no global round trip of their own outputs.
 __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p, int32_t force, int32_t run_greedy,
-                                                             int32_t *zero_counters, int32_t num_counters) {
+                                                             int32_t *zero_counters, int32_t num_counters,
+                                                             const int32_t *csr_indptr, const int32_t *csr_splits,
+                                                             int32_t csr_batch) {
     __shared__ PlanShared sh;
     extern __shared__ __align__(16) char dyn[];
     FusedLds &L = *reinterpret_cast<FusedLds *>(dyn);
@@ -675,8 +700,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p,
     const bool rules_lds = p.rule_count <= kLdsRules;
     const int32_t rule_v = p.rules[min((int)threadIdx.x, 5 * max(p.rule_count, 1) - 1)];
     const RowMirror mirror{L.a.rows.lengths, nullptr, L.a.rows.offsets, L.a.rows.chunk};
+    const CsrRows csr{csr_indptr, csr_splits, csr_batch, p.lengths, p.splits, p.active};
     stage_count_scan(p.lengths, p.splits, p.active, p.counts, p.offsets, p.chunk, p.record_count, p.error,
-                     p.batch_capacity, p.max_splits, p.max_context, sh, &mirror);
+                     p.batch_capacity, p.max_splits, p.max_context, sh, &mirror, csr_indptr ? &csr : nullptr);
     if (rules_lds && (int)threadIdx.x < 5 * p.rule_count) sh.rules[threadIdx.x] = rule_v;
     if (p.tile_prefix && p.span && p.span_units > 0) {
         // region B (the record weights, written from emission on) holds the prefix meanwhile
@@ -787,8 +813,11 @@ extern "C" int sgd_greedy_lists(const int32_t *weight, const int32_t *record_cou
     return launch_status("greedy_lists");
 }
 
-extern "C" int sgd_build_plan(const sgd_plan_buffers *plan, int32_t force_mode, int32_t run_greedy,
-                              int32_t *zero_counters, int32_t num_counters, void *stream) {
+namespace {
+
+int launch_build_plan(const sgd_plan_buffers *plan, int32_t force_mode, int32_t run_greedy, int32_t *zero_counters,
+                      int32_t num_counters, const int32_t *kv_indptr, const int32_t *num_kv_splits, int32_t batch,
+                      void *stream) {
     if (!plan) return einval("build_plan: null plan");
     if (int rc = check_plan_geometry(plan->batch_capacity, plan->max_splits, plan->kv_heads, plan->workers,
                                      plan->buckets))
@@ -803,6 +832,23 @@ extern "C" int sgd_build_plan(const sgd_plan_buffers *plan, int32_t force_mode, 
     if (int rc = prepare_plan_launch()) return rc;
     clear_stale_error();
     hipLaunchKernelGGL(k_build_plan, dim3(1), dim3(kPlanThreads), sizeof(FusedLds), (hipStream_t)stream, *plan,
-                       force_mode, run_greedy, zero_counters, num_counters);
+                       force_mode, run_greedy, zero_counters, num_counters, kv_indptr, num_kv_splits, batch);
     return launch_status("build_plan");
+}
+
+}  // namespace
+
+extern "C" int sgd_build_plan(const sgd_plan_buffers *plan, int32_t force_mode, int32_t run_greedy,
+                              int32_t *zero_counters, int32_t num_counters, void *stream) {
+    return launch_build_plan(plan, force_mode, run_greedy, zero_counters, num_counters, nullptr, nullptr, 0, stream);
+}
+
+extern "C" int sgd_build_plan_csr(const sgd_plan_buffers *plan, const int32_t *kv_indptr,
+                                  const int32_t *num_kv_splits, int32_t batch, int32_t force_mode,
+                                  int32_t run_greedy, int32_t *zero_counters, int32_t num_counters, void *stream) {
+    if (!kv_indptr || !num_kv_splits) return einval("build_plan_csr: kv_indptr and num_kv_splits are required");
+    if (plan && (batch < 0 || batch > plan->batch_capacity))
+        return einval("build_plan_csr: batch %d outside [0, %d]", batch, plan->batch_capacity);
+    return launch_build_plan(plan, force_mode, run_greedy, zero_counters, num_counters, kv_indptr, num_kv_splits,
+                             batch, stream);
 }

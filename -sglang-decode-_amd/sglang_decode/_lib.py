@@ -52,6 +52,7 @@ _SIGNATURES = {
     "sgd_order_and_packs": (_I, [_P] * 7 + [_P, _I, _I, _I, _I, _I, _I, _P]),
     "sgd_greedy_lists": (_I, [_P] * 5 + [_I] * 3 + [_P]),
     "sgd_build_plan": (_I, [ctypes.POINTER(PlanBuffersC), _I, _I, _P, _I, _P]),
+    "sgd_build_plan_csr": (_I, [ctypes.POINTER(PlanBuffersC), _P, _P, _I, _I, _I, _P, _I, _P]),
     "sgd_persistent_decode": (_I, [ctypes.POINTER(DecodeArgsC), _P]),
     "sgd_attention_kernel": (_I, [ctypes.POINTER(DecodeArgsC)]),
     "sgd_merge_splits": (_I, [_P] * 6 + [_I] * 5 + [_P]),

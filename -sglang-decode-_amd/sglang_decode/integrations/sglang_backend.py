@@ -16,7 +16,10 @@ STATIC|D1|D4 forces a schedule; DECODE_POLICY=<validated policy json>;
 DECODE_BATCH_CAPACITY (default 64); DECODE_REUSE_PLAN=0 rebuilds the plan on
 every layer; DECODE_WORKERS overrides the persistent worker count (default: two
 per compute unit); DECODE_FUSED_KV=0 keeps upstream's set_kv_buffer and a separate
-q copy instead of the one-launch KV write + q staging (kernels/kv_store.py).
+q copy instead of the one-launch KV write + q staging (kernels/kv_store.py);
+DECODE_FUSED_META=0 keeps the reference's per-step copies of kv_indptr differences
+and num_kv_splits into the plan (and the active fill) instead of the plan launch
+reading them itself (sgd_build_plan_csr).
 """
 import os
 
@@ -63,7 +66,8 @@ def layer_eligible(layer, config):
 
 
 def _fused_device(t):
-    """The one-launch KV write + q staging runs on the GPU library."""
+    """The fused launches (KV write + q staging, the plan reading the CSR metadata) run on
+    the GPU library only."""
     return t.device.type == "cuda"
 
 
@@ -78,6 +82,7 @@ def make_backend_class(base):
             self._eligible_step = False
             self.reuse_plan = os.getenv("DECODE_REUSE_PLAN", "1") == "1"
             self.fused_kv = os.getenv("DECODE_FUSED_KV", "1") == "1"
+            self.fused_meta = os.getenv("DECODE_FUSED_META", "1") == "1"
             found = eligible_model(model_runner, self.num_head, self.num_kv_head)
             if found is None:
                 return
@@ -101,7 +106,8 @@ def make_backend_class(base):
             self._prepared = False
             self._eligible_step = (self.scheduled is not None and decode and spec_info is None
                                    and 0 < bs <= self.scheduled.config.batch_capacity)
-            if self._eligible_step:
+            # with the fused metadata read the plan launch sets active itself
+            if self._eligible_step and not (self.fused_meta and _fused_device(self.scheduled.plan.active)):
                 self.scheduled.plan.active.fill_(bs)
 
         def init_forward_metadata(self, forward_batch):
@@ -148,9 +154,13 @@ def make_backend_class(base):
                     pool.set_kv_buffer(layer, forward_batch.out_cache_loc, k, v)
             meta, p = self.forward_metadata, engine.plan
             if not self._prepared or not self.reuse_plan:
-                p.lengths[:batch].copy_(meta.kv_indptr[1:batch + 1] - meta.kv_indptr[:batch])
-                p.splits[:batch].copy_(meta.num_kv_splits[:batch])
-                engine.prepare()
+                if self.fused_meta and _fused_device(p.active):
+                    # lengths = kv_indptr differences, splits and active read inside the plan launch
+                    engine.prepare(csr_metadata=(meta.kv_indptr, meta.num_kv_splits, batch))
+                else:
+                    p.lengths[:batch].copy_(meta.kv_indptr[1:batch + 1] - meta.kv_indptr[:batch])
+                    p.splits[:batch].copy_(meta.num_kv_splits[:batch])
+                    engine.prepare()
                 self._prepared = True
             qbuf = self.query_buffers[layer.layer_id]
             q_view = q.view(batch, c.query_heads, c.head_dim)

@@ -13,19 +13,26 @@ results; used by the parity tests of each stage).
 from ..kernels import plan as K
 
 
-def build_plan(plan, force_mode=-1, *, fused=True, counters=None, spans=False):
+def build_plan(plan, force_mode=-1, *, fused=True, counters=None, spans=False, csr_metadata=None):
     """``spans``: the fused build also writes the span schedule's tables (only the span
-    kernel reads them)."""
+    kernel reads them).  ``csr_metadata`` = (kv_indptr, num_kv_splits, batch): the fused
+    build reads the step's lengths, split counts and batch from them (no copies into the
+    plan beforehand); the staged path makes those copies itself."""
     force_mode = int(force_mode)
     run_greedy = force_mode == 2 or any_static_rule(plan)
     if fused:
-        K.fused_build(plan, force_mode, run_greedy, counters, spans)
+        K.fused_build(plan, force_mode, run_greedy, counters, spans, csr_metadata)
         plan.dispatch_valid = True
         plan.span_valid = bool(spans)
         return
     plan.dispatch_valid = plan.span_valid = False  # the stage launches write neither table
     if counters is not None:
         counters.zero_()
+    if csr_metadata is not None:
+        indptr, splits, batch = csr_metadata
+        plan.lengths[:batch].copy_(indptr[1:batch + 1] - indptr[:batch])
+        plan.splits[:batch].copy_(splits[:batch])
+        plan.active.fill_(batch)
     K.count_scan(plan)
     if force_mode == 0:
         plan.mode.fill_(0)

@@ -79,6 +79,9 @@ def parse():
     ap.add_argument("--kv-store", action="store_true",
                     help="also time the decode step's KV-pool write + q staging: one launch "
                          "(kernels/kv_store.py) against upstream's two scatters and a copy")
+    ap.add_argument("--plan-inputs", action="store_true",
+                    help="also time the plan build reading kv_indptr / num_kv_splits itself against the "
+                         "reference adapter's copies before it")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run a plain N-MiB read+write kernel 5 times, so a rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE pass can scale its counts to bytes")
@@ -168,6 +171,38 @@ def time_kv_store(c, fx, graph, batch, layers, csr, dtype, dev, reps=32, rounds=
     out = {name: round(graph_time(fn, reps, dev, rounds), 2) for name, fn in (("fused_us", fused),
                                                                               ("separate_us", separate))}
     out["tokens"] = batch
+    return out
+
+
+def time_plan_inputs(c, lengths, splits, dev, reps=32, rounds=5):
+    """The per-step plan build from the step's CSR metadata: what the reference adapter
+    runs (integrations/sglang_backend.py:50-55, 98-99: the active fill, lengths as
+    kv_indptr differences, the num_kv_splits copy, then the plan launch) against the one
+    launch that reads kv_indptr / num_kv_splits itself (sgd_build_plan_csr).  Each
+    captured in a HIP graph of `reps` builds, replayed between HIP events; median."""
+    import torch
+    from sglang_decode.planning.builder import build_plan
+    from sglang_decode.runtime.workspace import PlanBuffers
+    plan = PlanBuffers(c, dev)
+    sync = torch.zeros(2, dtype=torch.int32, device=dev)
+    b = len(lengths)
+    indptr = torch.zeros(b + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(torch.tensor(lengths, dtype=torch.int64), 0).to(torch.int32)
+    indptr = indptr.to(dev)
+    num = torch.tensor(splits, dtype=torch.int32, device=dev)
+
+    def copies(_):
+        plan.active.fill_(b)
+        plan.lengths[:b].copy_(indptr[1:b + 1] - indptr[:b])
+        plan.splits[:b].copy_(num[:b])
+        build_plan(plan, -1, counters=sync)
+
+    def fused(_):
+        build_plan(plan, -1, counters=sync, csr_metadata=(indptr, num, b))
+
+    out = {name: round(graph_time(fn, reps, dev, rounds), 2) for name, fn in (("fused_us", fused),
+                                                                              ("copies_us", copies))}
+    out["batch"] = b
     return out
 
 
@@ -378,6 +413,11 @@ def main():
     print(f"[bench] attention + merge ({best}): {attn_merge_us:.2f} us/layer; single-layer full entry "
           f"(plan + attention + merge): {single_layer_us:.2f} us", flush=True)
 
+    plan_inputs = None
+    if args.plan_inputs:
+        plan_inputs = time_plan_inputs(c, lengths, splits, dev)
+        print(f"[bench] plan build per step: reading the CSR metadata {plan_inputs['fused_us']:.2f} us, "
+              f"copies + build {plan_inputs['copies_us']:.2f} us", flush=True)
     kv_store = None
     if args.kv_store:
         kv_store = time_kv_store(c, fx, graph, batch, layers, csr, dtype, dev)
@@ -432,6 +472,8 @@ def main():
     }
     if kv_store is not None:
         line["kv_store"] = kv_store
+    if plan_inputs is not None:
+        line["plan_inputs"] = plan_inputs
     text = json.dumps(line)
     if args.json_out:
         with open(args.json_out, "w") as f:

@@ -144,6 +144,23 @@ typedef struct sgd_plan_buffers {
 int sgd_build_plan(const sgd_plan_buffers *plan, int32_t force_mode, int32_t run_greedy,
                    int32_t *zero_counters, int32_t num_counters, void *stream);
 
+/*
+ * sgd_build_plan with the plan's inputs taken from the step's CSR metadata: replaces
+ * the reference adapter's per-step copies before the build
+ * (integrations/sglang_backend.py:98-99: plan.lengths[:batch] = kv_indptr[1:batch+1]
+ * - kv_indptr[:batch], plan.splits[:batch] = num_kv_splits[:batch]) and the active
+ * fill of its metadata hook (:50-55) with reads inside the same launch.  Rows r <
+ * batch of plan->lengths / plan->splits and *plan->active (= batch) are also written,
+ * as the copies would have; rows >= batch are left as they are (unused).  kv_indptr
+ * [>= batch + 1] and num_kv_splits [>= batch] are device int32; 0 <= batch <=
+ * batch_capacity.  Lengths and split counts are validated exactly as for
+ * sgd_build_plan (a negative length or a split count outside [1, max_splits] sets
+ * error).
+ */
+int sgd_build_plan_csr(const sgd_plan_buffers *plan, const int32_t *kv_indptr, const int32_t *num_kv_splits,
+                       int32_t batch, int32_t force_mode, int32_t run_greedy, int32_t *zero_counters,
+                       int32_t num_counters, void *stream);
+
 /* Arguments of one persistent decode-attention launch. */
 typedef struct sgd_decode_args {
     const void *q, *k, *v;          /* q [bcap,Hq,D]; k/v paged [P,page,Hkv,D] or CSR [tok,Hkv,D] */

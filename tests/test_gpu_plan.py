@@ -114,6 +114,58 @@ def test_plan_zero_batch_and_edges():
             run_case(c, lengths, splits, force, True)
 
 
+def run_csr_case(c, lengths, splits, force, name=""):
+    """sgd_build_plan_csr: the plan built from (kv_indptr, num_kv_splits, batch) inside the
+    launch equals the oracle's plan of those rows, and the plan's lengths / splits rows <
+    batch and active hold what the reference adapter's copies would (integrations/
+    sglang_backend.py:98-99); rows >= batch are not touched."""
+    plan = PlanBuffers(c, "cuda")
+    for t in (plan.lengths, plan.splits, plan.active):
+        t.fill_(-5)
+    poison(plan)
+    n = len(lengths)
+    indptr = torch.zeros(n + 4, dtype=torch.int32)  # entries past batch + 1 must not matter
+    indptr[1:n + 1] = torch.cumsum(torch.tensor(lengths, dtype=torch.int64), 0).to(torch.int32)
+    indptr[n + 1:] = -999
+    sp = torch.tensor(list(splits) + [77] * 3, dtype=torch.int32)
+    build_plan(plan, force, csr_metadata=(indptr.cuda(), sp.cuda(), n))
+    dev = read_plan(plan)
+    lw = list(lengths) + [0] * (c.batch_capacity - n)
+    sw = list(splits) + [1] * (c.batch_capacity - n)
+    assert_plan_equal(dev, OP.full_plan(lw, sw, n, cfg_ns(c), [], force), c, n, f"{name} force={force} csr")
+    assert plan.lengths[:n].tolist() == list(lengths) and plan.splits[:n].tolist() == list(splits)
+    assert (plan.lengths[n:] == -5).all() and (plan.splits[n:] == -5).all() and plan.active.item() == n
+    return dev
+
+
+def test_plan_from_csr_metadata_matches_oracle():
+    for name in ("c1", "c2", "c3", "c5"):
+        c = W.config_for(name)
+        lengths = W.lengths_for(name)
+        splits = W.splits_for(name, lengths, c)
+        for force in FORCES:
+            run_csr_case(c, lengths, splits, force, name)
+            run_csr_case(c, lengths[:len(lengths) // 2 + 1], splits[:len(lengths) // 2 + 1], force, name)
+    c = DecodeConfig(batch_capacity=8, max_context=1024, workers=16)
+    for force in FORCES:
+        run_csr_case(c, [], [], force, "empty")
+    # invalid rows: a decreasing kv_indptr (negative length), split counts outside [1, 16]
+    for lengths, splits in (([10, -3, 5], [1, 1, 1]), ([10, 20], [1, 17]), ([10, 20], [0, 1])):
+        dev = run_csr_case(c, lengths, splits, -1, "invalid")
+        assert dev["error"] == 1 and dev["record_count"] == 0
+
+
+def test_plan_from_csr_metadata_rejects_bad_arguments():
+    c = DecodeConfig(batch_capacity=8, max_context=1024, workers=16)
+    plan = PlanBuffers(c, "cuda")
+    indptr = torch.zeros(9, dtype=torch.int32, device="cuda")
+    splits = torch.ones(8, dtype=torch.int32, device="cuda")
+    for meta in ((indptr, splits, 9), (indptr, splits, -1), (indptr[:3], splits, 3), (indptr.long(), splits, 2),
+                 (indptr, splits.cpu(), 2)):
+        with pytest.raises(ValueError):
+            build_plan(plan, -1, csr_metadata=meta)
+
+
 def test_fused_plan_clears_counters():
     c = W.config_for("c1")
     plan = PlanBuffers(c, "cuda")

@@ -89,7 +89,7 @@ def layer(layer_id, heads=32, kv_heads=8, head_dim=128, **kw):
 @pytest.fixture(autouse=True)
 def clean_env(monkeypatch):
     for name in ("DECODE_DISABLE", "DECODE_MODE", "DECODE_POLICY", "DECODE_BATCH_CAPACITY",
-                 "DECODE_REUSE_PLAN", "DECODE_WORKERS", "DECODE_FUSED_KV"):
+                 "DECODE_REUSE_PLAN", "DECODE_WORKERS", "DECODE_FUSED_KV", "DECODE_FUSED_META"):
         monkeypatch.delenv(name, raising=False)
 
 
@@ -127,13 +127,14 @@ class Recorder:
     """Stands in for the engine's device work on a CPU-only host."""
 
     def __init__(self, engine):
-        self.prepares, self.executes = 0, []
+        self.prepares, self.executes, self.metadata = 0, [], []
         engine.prepare = self.prepare
         engine.execute = self.execute
         self.engine = engine
 
-    def prepare(self):
+    def prepare(self, *, csr_metadata=None):
         self.prepares += 1
+        self.metadata.append(csr_metadata)
 
     def execute(self, q, k, v, pages, layer=0, *, indptr=None, scale=None):
         self.executes.append(dict(q=q.clone(), k=k, v=v, pages=pages, layer=layer, indptr=indptr,
@@ -180,6 +181,38 @@ def test_decode_step_data_flow_and_plan_reuse(monkeypatch, reuse):
     assert torch.equal(e["q"][:3], q.view(3, 32, 128))  # per-layer q buffer at capture capacity
     assert e["q"].shape == (64, 32, 128)
     assert b.mr_pool.writes == [0, 1]
+
+
+def test_fused_metadata_read_replaces_the_plan_copies(monkeypatch):
+    """With the plan launch reading kv_indptr / num_kv_splits itself (the default on the
+    GPU), the adapter makes no copies into the plan and no active fill; the plan build
+    gets the step's metadata and batch.  DECODE_FUSED_META=0 restores the copies."""
+    from sglang_decode.integrations import sglang_backend as SB
+    monkeypatch.setattr(SB, "_fused_device", lambda t: True)
+    monkeypatch.setenv("DECODE_FUSED_KV", "0")
+    b = make_backend()
+    rec = Recorder(b.scheduled)
+    p = b.scheduled.plan
+    p.lengths.fill_(-7)
+    p.active.fill_(-7)
+    fb = decode_batch(b, [5, 17, 3], [1, 2, 1])
+    b.init_forward_metadata(fb)
+    assert p.active.item() == -7  # left to the plan launch
+    q = torch.randn(3, 32 * 128).to(torch.bfloat16)
+    for lid in range(2):
+        b.forward_decode(q, q, q, layer(lid), fb, save_kv_cache=False)
+    assert rec.prepares == 1 and (p.lengths == -7).all()
+    indptr, splits, batch = rec.metadata[0]
+    assert indptr is b.forward_metadata.kv_indptr and splits is b.forward_metadata.num_kv_splits and batch == 3
+    monkeypatch.setenv("DECODE_FUSED_META", "0")
+    b = make_backend()
+    rec = Recorder(b.scheduled)
+    fb = decode_batch(b, [5, 17, 3], [1, 2, 1])
+    b.init_forward_metadata(fb)
+    b.forward_decode(q, q, q, layer(0), fb, save_kv_cache=False)
+    p = b.scheduled.plan
+    assert rec.metadata == [None] and p.active.item() == 3
+    assert p.lengths[:3].tolist() == [5, 17, 3] and p.splits[:3].tolist() == [1, 2, 1]
 
 
 class StoreRecorder:
