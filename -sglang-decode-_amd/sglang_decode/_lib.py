@@ -53,6 +53,8 @@ _SIGNATURES = {
     "sgd_greedy_lists": (_I, [_P] * 5 + [_I] * 3 + [_P]),
     "sgd_build_plan": (_I, [ctypes.POINTER(PlanBuffersC), _I, _I, _P, _I, _P]),
     "sgd_build_plan_csr": (_I, [ctypes.POINTER(PlanBuffersC), _P, _P, _I, _I, _I, _P, _I, _P]),
+    "sgd_csr_metadata": (_I, [_P, _I, _P, _I, _P, ctypes.c_int64, ctypes.c_int64, _I, _I, _I, _P, _P,
+                              ctypes.c_int64, _P, _P, _P, _P, _P, _P]),
     "sgd_persistent_decode": (_I, [ctypes.POINTER(DecodeArgsC), _P]),
     "sgd_attention_kernel": (_I, [ctypes.POINTER(DecodeArgsC)]),
     "sgd_merge_splits": (_I, [_P] * 6 + [_I] * 5 + [_P]),

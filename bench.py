@@ -200,9 +200,30 @@ def time_plan_inputs(c, lengths, splits, dev, reps=32, rounds=5):
     def fused(_):
         build_plan(plan, -1, counters=sync, csr_metadata=(indptr, num, b))
 
-    out = {name: round(graph_time(fn, reps, dev, rounds), 2) for name, fn in (("fused_us", fused),
-                                                                              ("copies_us", copies))}
+    # From the request pool: kv_indptr / kv_indices / split counts and the plan's inputs in
+    # one launch (kernels/csr_metadata.py), then the build -- seq_lens to plan in two launches.
+    from sglang_decode.kernels.csr_metadata import csr_metadata
+    gen = torch.Generator().manual_seed(97)
+    req_to_token = torch.randint(0, 1 << 20, (b, max(lengths)), generator=gen, dtype=torch.int32).to(dev)
+    seq_lens = torch.tensor(lengths, dtype=torch.int64, device=dev)
+    pool_idx = torch.randperm(b, generator=gen).to(dev)
+    meta_indptr = torch.zeros(b + 1, dtype=torch.int32, device=dev)
+    meta_indices = torch.zeros(sum(lengths), dtype=torch.int32, device=dev)
+    meta_splits = torch.zeros(b, dtype=torch.int32, device=dev)
+
+    def from_pool(_):
+        csr_metadata(seq_lens, pool_idx, req_to_token, c.max_splits, meta_indptr, meta_indices, meta_splits,
+                     plan=plan)
+        build_plan(plan, -1, counters=sync)
+
+    def metadata_only(_):
+        csr_metadata(seq_lens, pool_idx, req_to_token, c.max_splits, meta_indptr, meta_indices, meta_splits,
+                     plan=plan)
+
+    out = {name: round(graph_time(fn, reps, dev, rounds), 2) for name, fn in (
+        ("fused_us", fused), ("copies_us", copies), ("from_pool_us", from_pool), ("metadata_us", metadata_only))}
     out["batch"] = b
+    out["tokens"] = sum(lengths)
     return out
 
 
@@ -417,7 +438,8 @@ def main():
     if args.plan_inputs:
         plan_inputs = time_plan_inputs(c, lengths, splits, dev)
         print(f"[bench] plan build per step: reading the CSR metadata {plan_inputs['fused_us']:.2f} us, "
-              f"copies + build {plan_inputs['copies_us']:.2f} us", flush=True)
+              f"copies + build {plan_inputs['copies_us']:.2f} us; from the request pool (metadata launch "
+              f"{plan_inputs['metadata_us']:.2f} us + build) {plan_inputs['from_pool_us']:.2f} us", flush=True)
     kv_store = None
     if args.kv_store:
         kv_store = time_kv_store(c, fx, graph, batch, layers, csr, dtype, dev)

@@ -161,6 +161,30 @@ int sgd_build_plan_csr(const sgd_plan_buffers *plan, const int32_t *kv_indptr, c
                        int32_t batch, int32_t force_mode, int32_t run_greedy, int32_t *zero_counters,
                        int32_t num_counters, void *stream);
 
+/*
+ * The step's CSR metadata from the request pool, in one launch (no counterpart in the
+ * reference, which consumes it: integrations/sglang_backend.py:98-107; upstream SGLang
+ * v0.4.6.post5 produces it in its triton backend's decode metadata hook).  For rows i <
+ * batch: kv_indptr[i+1] = kv_indptr[i] + L_i (kv_indptr[0] = 0), kv_indices[kv_indptr[i]
+ * + j] = req_to_token[req_pool_indices[i] * row_stride + j] for j < L_i, with L_i =
+ * seq_lens[i].  Split counts by the reference harness rule (benchmarks/workloads.py:
+ * 20-21): chunk = max(1, ceil(max L / max_splits)), S_i = clamp(ceil(L_i / chunk), 1,
+ * max_splits), written to num_kv_splits when non-NULL.  plan_lengths / plan_splits (both
+ * or neither) and plan_active, when non-NULL, receive L_i, S_i and batch: the plan's
+ * inputs, so that sgd_build_plan follows without copies.  seq_lens and
+ * req_pool_indices are int32 or int64 (flags); req_to_token is int32 [rows, row_stride]
+ * with cols usable tokens per row.  A row with L_i < 0, L_i > cols or a pool index outside
+ * [0, rows) counts as length 0 and sets *error (when non-NULL); a valid total above
+ * indices_capacity makes every row length 0 and sets *error.  Nothing is read or written
+ * out of bounds.  0 <= batch <= 4096.
+ */
+int sgd_csr_metadata(const void *seq_lens, int32_t seq_lens_is_int64, const void *req_pool_indices,
+                     int32_t pool_indices_is_int64, const int32_t *req_to_token, int64_t rows,
+                     int64_t row_stride, int32_t cols, int32_t batch, int32_t max_splits, int32_t *kv_indptr,
+                     int32_t *kv_indices, int64_t indices_capacity, int32_t *num_kv_splits,
+                     int32_t *plan_lengths, int32_t *plan_splits, int32_t *plan_active, int32_t *error,
+                     void *stream);
+
 /* Arguments of one persistent decode-attention launch. */
 typedef struct sgd_decode_args {
     const void *q, *k, *v;          /* q [bcap,Hq,D]; k/v paged [P,page,Hkv,D] or CSR [tok,Hkv,D] */
