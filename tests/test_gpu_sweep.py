@@ -3,8 +3,8 @@ each case draws its own configuration -- GQA group 1-16, head_dim 64/128/256, pa
 sizes 2-64 and a non-power-of-two 12) or CSR, batch capacity, worker count, max_splits,
 ragged lengths with empty rows and rows at max_context, per-request split counts, scale,
 dtype, schedule -- and runs it on every kernel that supports the shape (the reference's
-own tests fix one shape per test, tests/test_decode_attention.py; the sweep covers the
-combinations between them).  Each case prints its draw first, so a failure names it."""
+own tests fix their shapes, tests/gpu/test_decode.py; the sweep covers the combinations
+between them).  Each case prints its draw first, so a failure names it."""
 import numpy as np
 import pytest
 import torch
