@@ -98,12 +98,11 @@ __device__ __forceinline__ void merge_row(const float *__restrict__ partial, con
     store_row<DT, DPL>(out, row, den, acc, bad, lane);
 }
 
-// One workgroup of kSplitWaves waves per (request, kSplitWaves heads).  A request
-// whose rows hold at most kRowsInFlight splits has each wave merge one head's row (one
-// round trip for its data).  A longer row is cut into kSplitWaves contiguous split
-// ranges, merged by the waves side by side and combined in wave order through LDS, one
-// head after the other -- so a 64-split row costs a block's round trip, not four.  The
-// split count is the request's, so the branch is uniform over the workgroup.
+// One workgroup of kSplitWaves waves per (request, head).  A row with at most
+// kRowsInFlight splits is merged by wave 0 alone (one round trip for its data); a
+// longer one is cut into kSplitWaves contiguous split ranges, merged by the waves side
+// by side and combined in wave order through LDS -- so a 64-split row costs a block's
+// round trip, not four.
 constexpr int kSplitWaves = 4;
 
 template <int DT, int DPL>
@@ -115,45 +114,40 @@ __global__ __launch_bounds__(64 * kSplitWaves) void k_merge(const float *__restr
                                                             int32_t smax) {
     __shared__ float sm[kSplitWaves], sd[kSplitWaves], sacc[kSplitWaves][DPL * 64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = blockIdx.x, head0 = blockIdx.y * kSplitWaves;
+    const int r = blockIdx.x, head = blockIdx.y;
     const int32_t n = __builtin_amdgcn_readfirstlane(counts[r]);
     const bool bad = *error != 0;
+    const int64_t row = (int64_t)r * hq + head;
     if (n <= kRowsInFlight) {
-        if (head0 + wave < hq) merge_row<DT, DPL>(partial, lse, n, bad, out, (int64_t)r * hq + head0 + wave, smax, lane);
+        if (wave == 0) merge_row<DT, DPL>(partial, lse, n, bad, out, row, smax, lane);
         return;  // n is the workgroup's: no wave waits below
     }
     const int32_t q = (n + kSplitWaves - 1) / kSplitWaves;
-    const int heads = min(kSplitWaves, hq - head0);
-    for (int h = 0; h < heads; ++h) {  // uniform: every wave meets every barrier
-        const int64_t row = (int64_t)r * hq + head0 + h;
-        float m, den, acc[DPL];
-        merge_part<DPL>(partial, lse, row, smax, min(wave * q, n), min((wave + 1) * q, n), lane, m, den, acc);
-        if (lane == 0) {
-            sm[wave] = m;
-            sd[wave] = den;
-        }
-#pragma unroll
-        for (int i = 0; i < DPL; ++i) sacc[wave][lane * DPL + i] = acc[i];
-        lds_barrier();
-        if (wave == 0) {
-            float M = -INFINITY;
-#pragma unroll
-            for (int k = 0; k < kSplitWaves; ++k) M = fmaxf(M, sm[k]);
-            float D = 0.f, X[DPL];
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) X[i] = 0.f;
-#pragma unroll
-            for (int k = 0; k < kSplitWaves; ++k) {
-                if (sd[k] == 0.f) continue;  // an empty range
-                const float sc = __builtin_amdgcn_exp2f(sm[k] - M);
-                D += sd[k] * sc;
-#pragma unroll
-                for (int i = 0; i < DPL; ++i) X[i] += sacc[k][lane * DPL + i] * sc;
-            }
-            store_row<DT, DPL>(out, row, D, X, bad, lane);
-        }
-        lds_barrier();  // the combine has read the shared state before the next head writes it
+    float m, den, acc[DPL];
+    merge_part<DPL>(partial, lse, row, smax, min(wave * q, n), min((wave + 1) * q, n), lane, m, den, acc);
+    if (lane == 0) {
+        sm[wave] = m;
+        sd[wave] = den;
     }
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) sacc[wave][lane * DPL + i] = acc[i];
+    lds_barrier();
+    if (wave != 0) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kSplitWaves; ++k) M = fmaxf(M, sm[k]);
+    float D = 0.f, X[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) X[i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < kSplitWaves; ++k) {
+        if (sd[k] == 0.f) continue;  // an empty range
+        const float sc = __builtin_amdgcn_exp2f(sm[k] - M);
+        D += sd[k] * sc;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) X[i] += sacc[k][lane * DPL + i] * sc;
+    }
+    store_row<DT, DPL>(out, row, D, X, bad, lane);
 }
 
 // The common case of the span merge in two memory round trips: the row's split
@@ -348,7 +342,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void k_merge_span(
 template <int DT>
 int launch_merge(const float *partial, const float *lse, const int32_t *counts, const int32_t *error, void *out,
                  int32_t bcap, int32_t hq, int32_t d, int32_t smax, hipStream_t stream) {
-    const dim3 grid(bcap, (hq + kSplitWaves - 1) / kSplitWaves), block(64 * kSplitWaves);
+    const dim3 grid(bcap, hq), block(64 * kSplitWaves);
     auto *o = static_cast<uint16_t *>(out);
     switch (d) {
         case 64: hipLaunchKernelGGL((k_merge<DT, 1>), grid, block, 0, stream, partial, lse, counts, error, o, hq, smax); break;
