@@ -230,8 +230,9 @@ def time_plan_inputs(c, lengths, splits, dev, reps=32, rounds=5):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this path needs "
-              "no collective; see DESIGN.md for how it would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the decode path "
+              "has no collective; each GPU would run its own share of the batch or of the KV heads)",
+              file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
