@@ -79,6 +79,10 @@ def parse():
     ap.add_argument("--kv-store", action="store_true",
                     help="also time the decode step's KV-pool write + q staging: one launch "
                          "(kernels/kv_store.py) against upstream's two scatters and a copy")
+    ap.add_argument("--rounds", type=int, default=3, help="timed rounds per schedule (median reported)")
+    ap.add_argument("--samples-csv", default="",
+                    help="write one row per schedule and round (variant, trial, iterations, gpu_us, wall_us, "
+                         "status: per step of all layers) for planning.calibrate")
     ap.add_argument("--plan-inputs", action="store_true",
                     help="also time the plan build reading kv_indptr / num_kv_splits itself against the "
                          "reference adapter's copies before it")
@@ -282,6 +286,7 @@ def main():
 
     results = {}
     engines = {}
+    samples = []
     host_lpt_us = None
     for name in [p for p in args.policies.split(",") if p]:
         host_static = name == "STATIC_HOST"
@@ -306,15 +311,21 @@ def main():
             graph.replay()
         torch.cuda.synchronize()
         rounds = []
-        for _ in range(3):
+        for trial in range(args.rounds):
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
+            wall0 = time.perf_counter_ns()
             start.record()
             for _ in range(args.steps):
                 graph.replay()
             end.record()
             end.synchronize()
             rounds.append(start.elapsed_time(end) / args.steps)
+            # STATIC_HOST is the reference benchmark's STATIC_CPU variant
+            samples.append(dict(variant="STATIC_CPU" if host_static else name, trial=trial, iterations=args.steps,
+                                gpu_us=round(rounds[-1] * 1000.0, 3),
+                                wall_us=round((time.perf_counter_ns() - wall0) / 1000.0 / args.steps, 3),
+                                status="ok"))
         ms_step = statistics.median(rounds)
         us_layer = ms_step * 1000.0 / layers
         results[name] = dict(ms_per_step=ms_step, us_per_layer=us_layer,
@@ -323,6 +334,12 @@ def main():
         print(f"[bench] {name}: {us_layer:.2f} us/layer  {results[name]['gbps']:.0f} GB/s "
               f"({100 * results[name]['gbps'] / PEAK_HBM_GBS:.1f}% of peak)", flush=True)
 
+    if args.samples_csv:
+        import csv
+        with open(args.samples_csv, "w", newline="") as f:
+            w = csv.DictWriter(f, fieldnames=["variant", "trial", "iterations", "gpu_us", "wall_us", "status"])
+            w.writeheader()
+            w.writerows(samples)
     best = min(results, key=lambda k: results[k]["us_per_layer"])
     engine, graph = engines[best]
 
