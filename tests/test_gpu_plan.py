@@ -155,6 +155,46 @@ def test_plan_from_csr_metadata_matches_oracle():
         assert dev["error"] == 1 and dev["record_count"] == 0
 
 
+def test_plan_from_csr_metadata_under_graph_replay():
+    """The adapter's use under graph capture: one captured build reading fixed kv_indptr /
+    num_kv_splits buffers whose contents change between replays (eager copies in between);
+    every replay's plan equals the oracle plan of the current contents."""
+    c = DecodeConfig(batch_capacity=8, max_context=1024, workers=16)
+    plan = PlanBuffers(c, "cuda")
+    sync = torch.zeros(2, dtype=torch.int32, device="cuda")
+    batch = 5
+    indptr = torch.zeros(batch + 1, dtype=torch.int32, device="cuda")
+    splits = torch.ones(batch, dtype=torch.int32, device="cuda")
+
+    def fill(lengths, sp):
+        ip = torch.zeros(batch + 1, dtype=torch.int32)
+        ip[1:] = torch.cumsum(torch.tensor(lengths), 0)
+        indptr.copy_(ip)
+        splits.copy_(torch.tensor(sp, dtype=torch.int32))
+
+    steps = [([100, 1024, 3, 0, 512], [2, 16, 1, 1, 4]), ([1, 1, 1, 1, 1], [1, 1, 1, 1, 1]),
+             ([900, 17, 640, 33, 1000], [8, 1, 5, 2, 16]), ([1024] * 5, [16] * 5)]
+    fill(*steps[0])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        build_plan(plan, -1, counters=sync, csr_metadata=(indptr, splits, batch))
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            build_plan(plan, -1, counters=sync, csr_metadata=(indptr, splits, batch))
+    torch.cuda.synchronize()
+    for lengths, sp in steps + steps[:1]:
+        fill(lengths, sp)
+        poison(plan)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        lw, sw = lengths + [0] * (c.batch_capacity - batch), sp + [1] * (c.batch_capacity - batch)
+        assert_plan_equal(read_plan(plan), OP.full_plan(lw, sw, batch, cfg_ns(c)), c, batch, str(lengths))
+        assert plan.lengths[:batch].tolist() == lengths and plan.active.item() == batch
+
+
 def test_plan_from_csr_metadata_rejects_bad_arguments():
     c = DecodeConfig(batch_capacity=8, max_context=1024, workers=16)
     plan = PlanBuffers(c, "cuda")
