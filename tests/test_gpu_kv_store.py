@@ -111,3 +111,74 @@ def test_adapter_writes_new_tokens_and_attends_them():
         assert torch.equal(keys[newest], k.view(4, 8, 128)) and torch.equal(values[newest], v.view(4, 8, 128))
         exp = OA.csr_attention(q.view(4, 32, 128), keys, values, indptr, perm, lengths, scale=0.125)
         close(out.view(4, 32, 128), exp[:4])
+
+
+def test_adapter_decode_under_graph_replay():
+    """SGLang's graph runner: the metadata hook, then every layer's forward_decode captured
+    once at a batch bucket and replayed after new contents of the runner's fixed buffers
+    (kv_indptr, kv_indices, num_kv_splits, out_cache_loc, q/k/v).  Each replay writes the
+    new tokens into the pools and attends them, with the plan read from the metadata inside
+    the captured plan launch (oracle on the pools after the write)."""
+    from oracle import attention as OA
+    from sglang_decode import workloads as W
+    from gpu_util import close
+    from test_sglang_adapter import Backend, FakeMode, layer, model_runner
+    bs, tokens, layers = 4, 4096, 2
+    mr = model_runner(device=DEV, tokens=tokens, layers=layers)
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    pool = mr.token_to_kv_pool
+    for t in pool.keys + pool.values:
+        t.copy_(torch.randn(t.shape, generator=gen, device=DEV, dtype=torch.float32))
+    pool.set_kv_buffer = None  # the fused launch must do the write
+    b = Backend(mr)
+    indptr = torch.zeros(bs + 1, dtype=torch.int32, device=DEV)
+    indices = torch.zeros(tokens, dtype=torch.int32, device=DEV)
+    splits = torch.ones(bs, dtype=torch.int32, device=DEV)
+    loc = torch.zeros(bs, dtype=torch.int64, device=DEV)
+    q = torch.zeros(bs, 32 * 128, dtype=torch.bfloat16, device=DEV)
+    kv = [(torch.zeros(bs, 8 * 128, dtype=torch.bfloat16, device=DEV),
+           torch.zeros(bs, 8 * 128, dtype=torch.bfloat16, device=DEV)) for _ in range(layers)]
+    b.forward_metadata = types.SimpleNamespace(kv_indptr=indptr, kv_indices=indices, num_kv_splits=splits)
+    fb = types.SimpleNamespace(batch_size=bs, forward_mode=FakeMode(True), spec_info=None, out_cache_loc=loc,
+                               token_to_kv_pool=pool)
+
+    def set_step(lengths, seed):
+        perm = torch.randperm(tokens, generator=torch.Generator().manual_seed(seed))[:sum(lengths)].to(torch.int32)
+        ip = torch.zeros(bs + 1, dtype=torch.int32)
+        ip[1:] = torch.cumsum(torch.tensor(lengths), 0)
+        indptr.copy_(ip)
+        indices[:perm.numel()].copy_(perm)
+        splits.copy_(torch.tensor(W.split_hints(lengths, 8), dtype=torch.int32))
+        loc.copy_(perm[ip[1:].long() - 1].to(torch.int64))  # each request's newest token
+        for x in [q] + [t for pair in kv for t in pair]:
+            x.copy_(torch.randn(x.shape, generator=gen, device=DEV, dtype=torch.float32))
+        return ip, perm
+
+    def run():
+        return [b.forward_decode(q, kv[lid][0], kv[lid][1], layer(lid), fb, save_kv_cache=True)
+                for lid in range(layers)]
+
+    steps = [[700, 33, 1, 2048], [1, 1, 1, 1], [1024, 1024, 1000, 1000], [5, 4000, 17, 64]]
+    set_step(steps[0], 0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        b.init_forward_metadata_capture_cuda_graph(bs, bs, None, None, None, FakeMode(True), None)
+        run()  # eager warm-up outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            outs = run()
+    torch.cuda.synchronize()
+    for i, lengths in enumerate(steps):
+        ip, perm = set_step(lengths, i + 1)
+        b.init_forward_metadata_replay_cuda_graph(bs, None, None, 0, None, FakeMode(True), None, None)
+        g.replay()
+        torch.cuda.synchronize()
+        newest = loc.long()
+        for lid in range(layers):
+            keys, values = pool.keys[lid], pool.values[lid]
+            assert torch.equal(keys[newest], kv[lid][0].view(bs, 8, 128))
+            assert torch.equal(values[newest], kv[lid][1].view(bs, 8, 128))
+            exp = OA.csr_attention(q.view(bs, 32, 128), keys, values, ip, perm, lengths, scale=0.125)
+            close(outs[lid].view(bs, 32, 128), exp[:bs], msg=f"step {i} layer {lid}")
