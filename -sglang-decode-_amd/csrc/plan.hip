@@ -208,36 +208,25 @@ __device__ __forceinline__ int bucket_of(int32_t w, int buckets) {
 }
 
 // ---------------------------------------------------------------- bucket tables
-// The bucket tables in registers: lane q (< kMaxBuckets) of every wave holds bucket q's
-// entries, so a sorted record position finds its bucket without LDS round trips.
-struct BucketRegs {
-    int32_t rbase, size, pbase, width, pp, pt;
-    __device__ BucketRegs(const PlanShared &sh, int lane) {
-        const int q = lane < kMaxBuckets ? lane : 0;
-        rbase = sh.bucket_record_base[q];
-        size = sh.bucket_size[q];
-        pbase = sh.bucket_pack_base[q];
-        width = sh.bucket_width[q];
-        pp = sh.bucket_packed_packs[q];
-        pt = sh.bucket_packed_tasks[q];
-    }
-};
-
 struct BucketOf {
     int32_t rbase, pbase, width, pp, pt;
 };
 
-// The bucket holding sorted record position j (buckets are laid out heaviest first).
-__device__ __forceinline__ BucketOf bucket_at(const BucketRegs &R, int32_t j, int buckets) {
+// The bucket holding sorted record position j (buckets are laid out heaviest first),
+// read from the LDS tables at uniform addresses.  The callers loop over tasks, so the
+// lanes past the last task are switched off: a per-lane register copy of the tables read
+// back with v_readlane would read those lanes' stale registers (the compiler loads the
+// copy inside the loop), while an LDS broadcast gives every active lane the table.
+__device__ __forceinline__ BucketOf bucket_at(const PlanShared &sh, int32_t j, int buckets) {
     BucketOf o{0, 0, 1, 0, 0};
     for (int q = buckets - 1; q >= 0; --q) {
-        const int32_t lo = __builtin_amdgcn_readlane(R.rbase, q), n = __builtin_amdgcn_readlane(R.size, q);
+        const int32_t lo = sh.bucket_record_base[q], n = sh.bucket_size[q];
         if (j >= lo && j < lo + n) {
             o.rbase = lo;
-            o.pbase = __builtin_amdgcn_readlane(R.pbase, q);
-            o.width = __builtin_amdgcn_readlane(R.width, q);
-            o.pp = __builtin_amdgcn_readlane(R.pp, q);
-            o.pt = __builtin_amdgcn_readlane(R.pt, q);
+            o.pbase = sh.bucket_pack_base[q];
+            o.width = sh.bucket_width[q];
+            o.pp = sh.bucket_packed_packs[q];
+            o.pt = sh.bucket_packed_tasks[q];
         }
     }
     return o;
@@ -392,10 +381,9 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
     // Pack tables, one task per thread (consecutive threads, consecutive tasks: the
     // stores of a wave land on neighbouring pack entries, not one record's Hkv tasks
     // per lane): a task that starts a pack writes it.
-    const BucketRegs R(sh, lane);
     const int32_t ntasks = wmul(total, hkv);
     for (int32_t task = tid; task < ntasks; task += kPlanThreads) {
-        const BucketOf o = bucket_at(R, task / hkv, buckets);
+        const BucketOf o = bucket_at(sh, task / hkv, buckets);
         int32_t count;
         const int32_t unit = pack_of(o, task, hkv, count);
         if (unit >= 0) {
@@ -506,7 +494,6 @@ __device__ void stage_dispatch_table(int32_t *table, int32_t capacity, const int
                                      int32_t buckets, const PlanShared &sh) {
     const int32_t mode = sh.mode;
     if (mode == 0) return;
-    const BucketRegs R(sh, threadIdx.x & 63);
     // one task per thread, so a wave writes neighbouring entries (the Hkv lanes of a
     // record find its request together: their LDS reads are broadcasts)
     const int32_t ntasks = wmul(total, hkv);
@@ -519,7 +506,7 @@ __device__ void stage_dispatch_table(int32_t *table, int32_t capacity, const int
         const int32_t b = wmul(s, c);
         const int32_t e = min(wadd(b, c), rows.lengths[r]);
         int32_t count = 1, unit = task;
-        if (mode >= 3) unit = pack_of(bucket_at(R, j, buckets), task, hkv, count);
+        if (mode >= 3) unit = pack_of(bucket_at(sh, j, buckets), task, hkv, count);
         if (unit < 0 || unit >= capacity) continue;
         int32_t *ent = table + 8 * (int64_t)unit;
         *reinterpret_cast<int4 *>(ent) = make_int4(task, count, r, s);

@@ -1,0 +1,112 @@
+"""Runs decode cases on the CPU executor and checks them against the oracle (test
+infrastructure).  Meant to run in its own process with the ASan build; ``spawn()``
+starts it with clang's ASan runtime preloaded.
+
+A case is a JSON object: {"sweep": seed} (the GPU sweep's draw of that seed, every
+kernel that takes its shape), or {"workload": "c1".."c5", "modes": [...], "kernels":
+[...], "requests": n} (a named configuration, optionally its first n requests).  One
+JSON line per (case, kernel, mode) goes to stdout: violations of the 2e-2 abs / 1e-2 rel
+tolerance, NaNs, nonzero rows past the batch, the plan compared bit-exactly with the
+oracle, and the claim counters left at zero.
+"""
+import json
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+TESTS = os.path.dirname(HERE)
+ROOT = os.path.dirname(TESTS)
+
+
+def spawn(cases, asan=True, timeout=900, env_extra=None):
+    """Run ``cases`` in a child process; returns (returncode, stdout, stderr)."""
+    import build as B
+    env = dict(os.environ)
+    if asan:
+        env["LD_PRELOAD"] = B.asan_runtime()
+        env["ASAN_OPTIONS"] = "detect_leaks=0:abort_on_error=1:halt_on_error=1:allocator_may_return_null=1"
+        env["ASAN_SYMBOLIZER_PATH"] = "/opt/rocm/llvm/bin/llvm-symbolizer"
+    env.update(env_extra or {})
+    cmd = [sys.executable, os.path.join(HERE, "run_cases.py"), "--asan" if asan else "--plain", json.dumps(cases)]
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout, env=env)
+    return p.returncode, p.stdout, p.stderr
+
+
+def _inputs(c, lengths, csr, seed, dtype):
+    from sglang_decode import workloads as W
+    from oracle import attention as OA
+    if csr:
+        q, k, v, indptr, indices = W.make_csr_inputs(c, lengths, seed=seed, dtype=dtype, device="cpu")
+        return (q, k, v, indices, indptr), lambda scale: OA.csr_attention(q, k, v, indptr, indices, lengths,
+                                                                           scale=scale)
+    q, k, v, pages = W.make_inputs(c, lengths, seed=seed, dtype=dtype, device="cpu")
+    return (q, k, v, pages, None), lambda scale: OA.paged_attention(q, k, v, pages, lengths, c.page_size,
+                                                                     scale=scale)
+
+
+def _check(emu, c, lengths, splits, inputs, expected, mode, kernel, scale, dtype_name, tag):
+    import numpy as np
+    import types
+    import driver as D
+    from oracle import plan as OP
+    r = D.decode(emu, c, lengths, splits, *inputs, mode=mode, kernel=kernel, scale=scale)
+    n = len(lengths)
+    o, e = r["out"][:n], expected[:n]
+    ns = types.SimpleNamespace(batch_capacity=c.batch_capacity, max_splits=c.max_splits,
+                               max_context=c.max_context, workers=c.workers, kv_heads=c.kv_heads,
+                               block_kv=c.block_kv)
+    ref = OP.full_plan(lengths, splits, n, ns, force=mode)
+    p = r["plan"]
+    plan_ok = (p["error"] == ref["error"] and p["record_count"] == ref["record_count"]
+               and p["counts"][:c.batch_capacity] == ref["counts"] and p["mode"] == ref["mode"]
+               and p["num_packs"] == ref["num_packs"])
+    if plan_ok and "request" in ref:
+        m = ref["record_count"]
+        plan_ok = all(p[k][:m] == ref[k][:m] for k in ("request", "split", "begin", "end", "weight"))
+        plan_ok = plan_ok and p["order"][:m] == ref["order"]
+        npk = ref["num_packs"]
+        plan_ok = plan_ok and p["pack_first"][:npk] == ref["pack_first"] and p["pack_count"][:npk] == ref[
+            "pack_count"]
+    return dict(case=tag, kernel=r["kernel"], mode=int(mode), dtype=dtype_name,
+                violations=int((np.abs(o - e) > 2e-2 + 1e-2 * np.abs(e)).sum()),
+                nans=int(np.isnan(o).sum()), tail=float(np.abs(r["out"][n:]).sum()),
+                plan_ok=bool(plan_ok), counters=r["sync"], max_err=float(np.nan_to_num(np.abs(o - e), nan=9.0).max())
+                if o.size else 0.0)
+
+
+def run(cases, asan):
+    import torch
+    import driver as D
+    sys.path.insert(0, TESTS)
+    emu = D.Emu(asan=asan)
+    for case in cases:
+        if "sweep" in case:
+            from test_gpu_sweep import draw, kernels_for
+            seed = int(case["sweep"])
+            c, csr, lengths, splits, dtype, mode, scale = draw(seed)
+            inputs, oracle = _inputs(c, lengths, csr, seed, dtype)
+            expected = oracle(scale)
+            for kernel in case.get("kernels") or kernels_for(c, csr):
+                print(json.dumps(_check(emu, c, lengths, splits, inputs, expected, int(mode), kernel, scale,
+                                        str(dtype), f"sweep {seed}")), flush=True)
+        else:
+            from sglang_decode import workloads as W
+            name = case["workload"]
+            c = W.config_for(name, workers=case.get("workers", 256))
+            lengths = W.lengths_for(name)[:case.get("requests")]
+            splits = W.split_hints(lengths, c.max_splits)
+            dtype = getattr(torch, case.get("dtype", "bfloat16"))
+            inputs, oracle = _inputs(c, lengths, c.page_size == 1, case.get("seed", 7), dtype)
+            expected = oracle(None)
+            for kernel in case.get("kernels", ["auto"]):
+                for mode in case.get("modes", [-1]):
+                    print(json.dumps(_check(emu, c, lengths, splits, inputs, expected, mode, kernel, None,
+                                            str(dtype), name)), flush=True)
+
+
+if __name__ == "__main__":
+    sys.path.insert(0, HERE)
+    for p in (os.path.join(ROOT, "-sglang-decode-_amd"), ROOT):
+        sys.path.insert(0, p)
+    run(json.loads(sys.argv[2]), asan=sys.argv[1] == "--asan")

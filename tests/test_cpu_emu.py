@@ -1,0 +1,104 @@
+"""The library's kernels executed on the CPU (tests/cpu_emu) under AddressSanitizer.
+
+Each thread of a workgroup runs as a fiber.  Cross-lane operations are evaluated over the
+lanes that reach them, and reading a lane that is switched off is an error.  Every
+buffer is an exact-size host allocation, so an access outside a buffer, the dynamic LDS
+block or a static LDS array aborts the run with the kernel, workgroup and thread named.
+
+What this pins:
+* The GPU memory fault of the sweep's seed 15 (max_splits 1, lengths [10, 15490], D4,
+  256 workers; 4 tasks, the heavy record in weight bucket 7).  The fused plan build's
+  pack-table and dispatch-table loops run one task per lane, so lanes past the last task
+  are switched off.  bucket_at() read the bucket tables with v_readlane from per-lane
+  registers, and the compiler loads those registers inside the loop, so bucket 7's entry
+  was read from lane 7's stale registers.  The garbage pack index was then stored
+  through (pack_first/pack_count/dispatch).  The executor rejects exactly that
+  inactive-lane read, so these cases fail if the pattern comes back.
+* The held sweep draws and the long-task draws run in bounds on every kernel that takes
+  their shape, match the FP32 oracle (2e-2 abs / 1e-2 rel), build the oracle's plan
+  bit-exactly and leave the claim counters at zero.
+"""
+import json
+import os
+import sys
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+EMU = os.path.join(HERE, "cpu_emu")
+if EMU not in sys.path:
+    sys.path.insert(0, EMU)
+
+
+@pytest.fixture(scope="module")
+def asan_build():
+    import build as B
+    return B.build(asan=True)
+
+
+def _run(cases, **kw):
+    import run_cases as R
+    rc, out, err = R.spawn(cases, **kw)
+    rows = [json.loads(line) for line in out.splitlines() if line.startswith("{")]
+    return rc, rows, err
+
+
+def _assert_clean(rc, rows, err, expected_rows):
+    assert rc == 0, f"executor run failed (rc {rc}):\n{err[-4000:]}"
+    assert "ERROR: AddressSanitizer" not in err, err[-4000:]
+    assert len(rows) == expected_rows, (len(rows), err[-2000:])
+    for r in rows:
+        assert r["violations"] == 0 and r["nans"] == 0, r
+        assert r["tail"] == 0.0, r        # rows past the batch are exact zeros
+        assert r["plan_ok"], r            # plan bit-exact against the oracle
+        assert r["counters"] == [0, 0], r  # claim / finished counters back at zero
+
+
+# (seed, kernels): the held max_splits-1 draws, then draws with the longest tasks.
+SWEEP = [(15, ["generic", "mfma", "valu"]), (16, ["generic"]), (17, ["generic", "mfma"]),
+         (21, ["generic", "mfma", "valu"]), (31, ["generic"]), (8, ["valu"]), (2, ["mfma"])]
+
+
+def test_sweep_draws_in_bounds(asan_build):
+    cases = [{"sweep": s, "kernels": k} for s, k in SWEEP]
+    rc, rows, err = _run(cases)
+    _assert_clean(rc, rows, err, sum(len(k) for _, k in SWEEP))
+
+
+def test_small_batch_every_mode_and_kernel(asan_build):
+    """Batch 4 at 8/2 heads: every schedule on every kernel, and the reversed workgroup
+    order (the dynamic schedules then hand the claims to other workers)."""
+    kernels, modes = ["generic", "mfma", "valu"], [0, 1, 2, 3, 4]
+    case = [{"workload": "c1", "kernels": kernels, "modes": modes}]
+    for env in (None, {"EMU_ORDER": "reverse"}):
+        rc, rows, err = _run(case, env_extra=env)
+        _assert_clean(rc, rows, err, len(kernels) * len(modes))
+
+
+def test_executor_reports_out_of_bounds(asan_build):
+    """The harness itself: an output buffer one row short makes the merge store past it,
+    and the run aborts with AddressSanitizer's report naming the kernel."""
+    import build as B
+    env = dict(os.environ, LD_PRELOAD=B.asan_runtime(), ASAN_OPTIONS="detect_leaks=0:abort_on_error=1")
+    code = r"""
+import ctypes, sys
+sys.path.insert(0, %r)
+import numpy as np
+import driver as D
+emu = D.Emu(asan=True)
+bcap, hq, d, smax = 2, 1, 64, 1
+partial = emu.array((bcap, hq, smax, d), np.float32, 0.5)
+lse = emu.array((bcap, hq, smax), np.float32, 0.0)
+counts = emu.array((bcap,), np.int32, 1)
+active = emu.array((1,), np.int32, bcap)
+error = emu.array((1,), np.int32, 0)
+out = emu.array((bcap * hq * d - 1,), np.uint16)   # one element short
+emu.lib.sgd_merge_splits(D.ptr(partial), D.ptr(lse), D.ptr(counts), D.ptr(active), D.ptr(error), D.ptr(out),
+                         bcap, hq, d, smax, 0, None)
+print("no report")
+""" % EMU
+    import subprocess
+    p = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
+    assert p.returncode != 0, p.stdout
+    assert "heap-buffer-overflow" in p.stderr, p.stderr[-3000:]
+    assert "k_merge" in p.stderr, p.stderr[-3000:]

@@ -1,0 +1,82 @@
+"""Parity at the benchmark configurations' full sizes, every request, on the product's
+defaults (AUTO kernel, two workers per CU), against the FP32 oracle (2e-2 abs / 1e-2 rel):
+
+* Llama-3-8B heads, batch 64, CSR page 1, lognormal lengths (median 1024): every schedule;
+* the skewed batch: 128 requests, 2 x 32768 + 126 x U[32, 512], up to 64 splits of at
+  most 512 tokens: D1 and D4;
+* Llama-3-70B heads, batch 32, page 16, lengths U[2048, 16384]: D1 and D4, bf16 and fp16.
+
+Partials and LSEs are NaN-poisoned before each launch, the plan's error flag, record
+count and per-row counts are compared with the planning spec, and the per-layer claim
+counters must be back at zero afterwards (reference: tests/gpu/test_decode.py:12-39)."""
+import pytest
+import torch
+
+from oracle import attention as OA
+from sglang_decode import workloads as W
+from sglang_decode.config import Mode, default_workers
+from sglang_decode.planning.reference import split_records
+from sglang_decode.runtime.engine import DecodeEngine
+
+from gpu_util import close
+
+pytestmark = pytest.mark.gpu
+
+_CACHE = {}
+
+
+def workload(name, dtype=torch.bfloat16):
+    key = (name, dtype)
+    if key not in _CACHE:
+        _CACHE.clear()  # one configuration's pools on the device at a time
+        torch.cuda.empty_cache()
+        c = W.config_for(name, workers=default_workers())
+        lengths = W.lengths_for(name)
+        splits = W.splits_for(name, lengths, c)
+        if c.page_size == 1:
+            q, k, v, indptr, indices = W.make_csr_inputs(c, lengths, seed=61, dtype=dtype)
+            expected = OA.csr_attention(q, k, v, indptr, indices, lengths)
+            inputs = (q, k, v, indices)
+        else:
+            q, k, v, pages = W.make_inputs(c, lengths, seed=61, dtype=dtype)
+            expected = OA.paged_attention(q, k, v, pages, lengths, c.page_size)
+            inputs, indptr = (q, k, v, pages), None
+        _CACHE[key] = (c, lengths, splits, inputs, indptr, expected)
+    return _CACHE[key]
+
+
+def check(name, mode, dtype=torch.bfloat16):
+    c, lengths, splits, inputs, indptr, expected = workload(name, dtype)
+    print(f"{name} mode={Mode(mode).name} dtype={dtype} batch={len(lengths)} total={sum(lengths)}", flush=True)
+    engine = DecodeEngine(c, dtype=dtype, force_mode=mode)
+    W.update_plan(engine, lengths, splits)
+    engine.layers[0].partial.fill_(float("nan"))
+    engine.layers[0].lse.fill_(float("nan"))
+    engine.prepare()
+    out = engine.execute(*inputs, indptr=indptr)
+    torch.cuda.synchronize()
+    records, counts, _ = split_records(lengths, splits, c)
+    assert engine.plan.error.item() == 0
+    assert engine.plan.record_count.item() == len(records)
+    assert engine.plan.counts[:len(lengths)].tolist() == counts
+    assert engine.sync.abs().sum().item() == 0  # claim / finished counters back at zero
+    close(out[:len(lengths)], expected[:len(lengths)], msg=f"{name} {Mode(mode).name} {dtype}")
+    return engine
+
+
+@pytest.mark.parametrize("mode", list(Mode))
+def test_llama8b_batch64_every_request(mode):
+    check("c2", mode)
+
+
+@pytest.mark.parametrize("mode", [Mode.D1, Mode.D4])
+def test_skewed_batch128_every_request(mode):
+    engine = check("c3", mode)
+    assert max(engine.plan.counts.tolist()) == 64  # the two long requests use all 64 splits
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode", [Mode.D1, Mode.D4])
+def test_llama70b_paged_batch32_every_request(mode, dtype):
+    engine = check("c4", mode, dtype)
+    assert engine.attention_kernel_name() == "mfma"

@@ -20,11 +20,6 @@ from gpu_util import close
 pytestmark = pytest.mark.gpu
 
 CASES = 40
-# Seed 15 (max_splits 1, a 15490-token task, D4 over 256 workers) ended in a GPU memory
-# fault whose cause reading the kernels, the plan build and the merge has not found; it
-# stays off the GPU until one is shown, and the other max_splits-1 draws wait with it.
-HELD = {15: "GPU memory fault with no cause found yet (max_splits 1, 15490-token task, D4)"}
-HELD_WITH = "max_splits 1, held back with seed 15 until that fault's cause is found"
 WORK_BUDGET = 32_000 * 32 * 128  # sum(lengths) x Hq x D per case: keeps the oracle to ~1 s
 
 
@@ -69,10 +64,6 @@ def kernels_for(c, csr):
 @pytest.mark.parametrize("seed", range(CASES))
 def test_random_configuration(seed):
     c, csr, lengths, splits, dtype, mode, scale = draw(seed)
-    if seed in HELD:
-        pytest.skip(HELD[seed])
-    if c.max_splits == 1:
-        pytest.skip(HELD_WITH)
     print(f"seed {seed}: {c} csr={csr} dtype={dtype} mode={mode.name} lengths={lengths} splits={splits}",
           flush=True)
     if csr:
