@@ -6,12 +6,8 @@
 namespace sgd {
 int launch_attention_generic(const sgd_decode_args &a, bool vec, hipStream_t stream);
 int launch_attention_valu(const sgd_decode_args &a, hipStream_t stream);
-int launch_attention_stream(const sgd_decode_args &a, hipStream_t stream);
 int launch_attention_mfma(const sgd_decode_args &a, hipStream_t stream);
-int launch_attention_span(const sgd_decode_args &a, hipStream_t stream);
 bool valu_supported(const sgd_decode_args &a);
-bool span_supported(const sgd_decode_args &a);
-bool stream_supported(const sgd_decode_args &a);
 bool mfma_supported(const sgd_decode_args &a);
 }
 
@@ -28,19 +24,6 @@ bool vector_layout(const sgd_decode_args &a) {
     for (int i = 0; i < 3; ++i)
         if (a.k_stride[i] % 8 != 0 || a.v_stride[i] % 8 != 0) return false;
     return true;
-}
-
-// Compute units of the current device (a host query, cached per device).
-int device_cus() {
-    static int cache[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (cache[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-        cache[dev] = n;
-    }
-    return cache[dev];
 }
 
 }  // namespace
@@ -65,10 +48,6 @@ int check_args(const sgd_decode_args *args) {
         return einval("persistent_decode: null buffer");
     if (a.dispatch && a.dispatch_units < 0)
         return einval("persistent_decode: dispatch_units %d < 0", a.dispatch_units);
-    if ((a.tile_prefix || a.span || a.edge) &&
-        (!a.tile_prefix || !a.span || !a.edge || a.batch_capacity <= 0 || a.span_units <= 0 || a.span_units % 8))
-        return einval("persistent_decode: the span schedule needs tile_prefix, span, edge, batch_capacity and "
-                      "span_units (a positive multiple of 8)");
     return 0;
 }
 
@@ -76,17 +55,11 @@ int check_args(const sgd_decode_args *args) {
 int resolve_kernel(const sgd_decode_args &a) {
     switch (a.kernel) {
         case SGD_KERNEL_AUTO:
-            // The stream kernel is one 1024-thread workgroup per CU: with more workers
-            // than CUs they would run in turns, so a two-per-CU kernel takes over --
-            // the VALU one for groups <= 4 (1-2% faster than the MFMA kernel, whose
-            // 16 MFMA columns are then three-quarters padding, on the Llama-3-8B
-            // layers measured), else the MFMA one (groups up to 16), else the
-            // generic kernel.  The span kernel runs on request only: on the
-            // Llama-3-8B batch-64 layer its static equal shares end unevenly within a
-            // workgroup (the waves' latencies differ), and with its edge-completing
-            // merge the layer takes 82.2 us against 76.7 us for the VALU kernel with
-            // dynamic claims.
-            if (stream_supported(a) && a.workers <= device_cus()) return SGD_KERNEL_STREAM;
+            // The VALU kernel for groups <= 4 (1-2% faster than the MFMA kernel, whose 16
+            // MFMA columns are then three-quarters padding, on the Llama-3-8B layers
+            // measured), else the MFMA one (groups up to 16), else the generic kernel.
+            // All three merge a task's wave states in a fixed order, so a launch is
+            // bitwise repeatable whatever the worker count.
             if (valu_supported(a)) return SGD_KERNEL_VALU;
             if (mfma_supported(a)) return SGD_KERNEL_MFMA;
             return SGD_KERNEL_GENERIC;
@@ -102,17 +75,6 @@ int resolve_kernel(const sgd_decode_args &a) {
                 return einval("persistent_decode: the MFMA kernel needs group <= 16, head_dim 128, unit dim "
                               "stride, 16-byte aligned rows and a power-of-two page size");
             return SGD_KERNEL_MFMA;
-        case SGD_KERNEL_SPAN:
-            if (!span_supported(a))
-                return einval("persistent_decode: the span kernel needs group <= 4, head_dim 128, unit dim "
-                              "stride, 16-byte aligned rows of q, K/V and partial, a power-of-two page size "
-                              "and the plan's span tables with an edge buffer");
-            return SGD_KERNEL_SPAN;
-        case SGD_KERNEL_STREAM:
-            if (!stream_supported(a))
-                return einval("persistent_decode: the stream kernel needs group <= 4, head_dim 128, unit dim "
-                              "stride, 16-byte aligned rows and partial, and a power-of-two page size");
-            return SGD_KERNEL_STREAM;
         default:
             return einval("persistent_decode: kernel %d not available", a.kernel);
     }
@@ -132,10 +94,6 @@ extern "C" int sgd_persistent_decode(const sgd_decode_args *args, void *stream) 
     if (kernel < 0) return kernel;
     clear_stale_error();
     switch (kernel) {
-        case SGD_KERNEL_SPAN:
-            return launch_attention_span(a, (hipStream_t)stream);
-        case SGD_KERNEL_STREAM:
-            return launch_attention_stream(a, (hipStream_t)stream);
         case SGD_KERNEL_VALU:
             return launch_attention_valu(a, (hipStream_t)stream);
         case SGD_KERNEL_MFMA:

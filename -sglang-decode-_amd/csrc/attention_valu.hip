@@ -20,11 +20,6 @@
 // normalized partial and natural-log LSE go to slot (request, head, split)
 // (kernels/attention.py:81-84).
 //
-// Two workgroup barriers per task bound this kernel: waves idle at the end of a
-// task whose tile count is not a multiple of kWaves, and the task's descriptor
-// chain is resolved while no KV load is in flight.  attention_stream.hip removes
-// both; this kernel stays as the simple baseline and the fallback for worker
-// counts above one per CU.
 #include "valu_ops.h"
 
 namespace sgd {

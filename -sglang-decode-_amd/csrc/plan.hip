@@ -12,7 +12,6 @@
 //   greedy_lists         kernels/plan.py:103-135 (same lists as planning/reference.py:57-67)
 // Integer arithmetic is int32 with wrap-around, like the reference's lanes.
 #include "common.h"
-#include "span_layout.h"
 
 namespace sgd {
 namespace {
@@ -514,101 +513,6 @@ __device__ void stage_dispatch_table(int32_t *table, int32_t capacity, const int
     }
 }
 
-// ---------------------------------------------------------------- span tables
-// Tables of the span schedule (attention_span.hip; no reference counterpart).  The
-// step's work is one sequence of 16-token tiles: requests in order, within a request
-// its splits, within a split its kv heads, within a head its tiles.  Request r holds
-// ceil(L_r / 16) tiles per kv head whatever its splits (every split but the last is a
-// multiple of 32 tokens), so tile_prefix[r] = sum over earlier rows of those counts
-// (0 for rows without records) locates every task without the record table, in every
-// mode.  Wave u of U takes tiles [X_u, X_{u+1}), X_u = floor(u * T / U),
-// T = kv_heads * tile_prefix[bcap]; its record (span_layout.h) holds where X_u sits --
-// request, split, kv head, tile -- and that request's geometry, so a wave starts
-// streaming after one load of its record.
-constexpr int kSpanTile = 16;
-constexpr int kSpanRecord = 16;
-
-__device__ void stage_spans(const RowMirror &rows, int32_t bcap, int32_t hkv, int32_t units,
-                            int32_t *tile_prefix, int32_t *span, int32_t *prefix_lds, PlanShared &sh) {
-    const int tid = threadIdx.x;
-    const int per = (bcap + kPlanThreads - 1) / kPlanThreads;
-    const int r0 = tid * per;
-    int32_t tiles[kMaxRowsPerThread], local = 0;
-#pragma unroll
-    for (int i = 0; i < kMaxRowsPerThread; ++i) {
-        tiles[i] = 0;
-        const int r = r0 + i;
-        if (i >= per || r >= bcap) continue;
-        const bool has = rows.offsets[r + 1] != rows.offsets[r];
-        tiles[i] = has ? cdiv(rows.lengths[r], kSpanTile) : 0;
-        local = wadd(local, tiles[i]);
-    }
-    int32_t total;
-    int32_t running = block_exclusive_scan<int32_t>(local, sh.scan_tmp, &total);
-#pragma unroll
-    for (int i = 0; i < kMaxRowsPerThread; ++i) {
-        const int r = r0 + i;
-        if (i >= per || r >= bcap) continue;
-        prefix_lds[r] = running;
-        tile_prefix[r] = running;
-        running = wadd(running, tiles[i]);
-    }
-    if (tid == 0) {
-        prefix_lds[bcap] = total;
-        tile_prefix[bcap] = total;
-    }
-    lds_barrier();
-    const int64_t T = (int64_t)hkv * total;
-    for (int u = tid; u < units; u += kPlanThreads) {
-        const int32_t x0 = span::floor_div((int64_t)u * T, units), x1 = span::floor_div((int64_t)(u + 1) * T, units);
-        int32_t rec[kSpanRecord];
-#pragma unroll
-        for (int k = 0; k < kSpanRecord; ++k) rec[k] = 0;
-        rec[0] = x0;
-        rec[1] = x1;
-        rec[2] = bcap;
-        if (x0 < x1) {
-            // the request holding tile x0: smallest r' in [1, bcap] with hkv * prefix[r'] > x0, less one
-            int lo = 1, hi = bcap;
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if ((int64_t)hkv * prefix_lds[mid] > x0) hi = mid;
-                else lo = mid + 1;
-            }
-            const int r = lo - 1;
-            const int32_t p0 = prefix_lds[r], per_head = prefix_lds[r + 1] - p0;
-            const int32_t c = rows.chunk[r], c16 = c / kSpanTile;
-            const int32_t n = rows.offsets[r + 1] - rows.offsets[r];
-            const int32_t local_x = x0 - hkv * p0, full = (n - 1) * hkv * c16;
-            int32_t sp, g, j;
-            if (local_x < full) {
-                sp = local_x / (hkv * c16);
-                const int32_t rem = local_x - sp * hkv * c16;
-                g = rem / c16;
-                j = rem - g * c16;
-            } else {
-                const int32_t nt_last = per_head - (n - 1) * c16;
-                sp = n - 1;
-                g = (local_x - full) / nt_last;
-                j = (local_x - full) - g * nt_last;
-            }
-            rec[2] = r;
-            rec[3] = sp;
-            rec[4] = g;
-            rec[5] = j;
-            rec[6] = p0;
-            rec[7] = per_head;
-            rec[8] = c;
-            rec[9] = n;
-            rec[10] = rows.lengths[r];
-        }
-        int4 *dst = reinterpret_cast<int4 *>(span + (int64_t)u * kSpanRecord);
-#pragma unroll
-        for (int k = 0; k < kSpanRecord / 4; ++k)
-            dst[k] = make_int4(rec[4 * k], rec[4 * k + 1], rec[4 * k + 2], rec[4 * k + 3]);
-    }
-}
-
 // ---------------------------------------------------------------- kernels
 __global__ __launch_bounds__(kPlanThreads) void k_count_scan(const int32_t *lengths, const int32_t *splits,
                                                              const int32_t *active, int32_t *counts,
@@ -691,11 +595,6 @@ __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p,
     stage_count_scan(p.lengths, p.splits, p.active, p.counts, p.offsets, p.chunk, p.record_count, p.error,
                      p.batch_capacity, p.max_splits, p.max_context, sh, &mirror, csr_indptr ? &csr : nullptr);
     if (rules_lds && (int)threadIdx.x < 5 * p.rule_count) sh.rules[threadIdx.x] = rule_v;
-    if (p.tile_prefix && p.span && p.span_units > 0) {
-        // region B (the record weights, written from emission on) holds the prefix meanwhile
-        lds_barrier();
-        stage_spans(mirror, p.batch_capacity, p.kv_heads, p.span_units, p.tile_prefix, p.span, L.b.weight, sh);
-    }
     if (force == 0) {  // forced R0: counts/offsets only (planning/builder.py:11-14)
         if (threadIdx.x == 0) { *p.mode = 0; *p.num_packs = 0; }
         return;
@@ -810,11 +709,6 @@ int launch_build_plan(const sgd_plan_buffers *plan, int32_t force_mode, int32_t 
                                      plan->buckets))
         return rc;
     if (plan->rule_count < 0) return einval("build_plan: negative rule_count");
-    if ((plan->tile_prefix || plan->span) &&
-        (!plan->tile_prefix || !plan->span || plan->span_units <= 0 || plan->span_units % 8 != 0))
-        return einval("build_plan: span tables need both buffers and span_units a positive multiple of 8");
-    if (plan->span && (reinterpret_cast<uintptr_t>(plan->span) & 15))
-        return einval("build_plan: span table not 16-byte aligned");
     if (num_counters < 0 || (num_counters > 0 && !zero_counters)) return einval("build_plan: counters");
     if (int rc = prepare_plan_launch()) return rc;
     clear_stale_error();

@@ -14,7 +14,7 @@ from ._build import LIB_PATH
 
 SGD_EINVAL = -22
 SGD_BF16, SGD_FP16 = 0, 1
-KERNELS = {"auto": 0, "generic": 1, "valu": 2, "mfma": 3, "stream": 4, "span": 5}
+KERNELS = {"auto": 0, "generic": 1, "valu": 2, "mfma": 3}
 KERNEL_NAMES = {v: k for k, v in KERNELS.items()}
 
 _P = ctypes.c_void_p
@@ -25,9 +25,9 @@ class PlanBuffersC(ctypes.Structure):
     _fields_ = [(name, _P) for name in (
         "lengths", "splits", "active", "counts", "offsets", "chunk", "request", "split", "begin",
         "end", "weight", "order", "pack_first", "pack_count", "record_count", "num_packs", "mode",
-        "error", "static_head", "static_next", "rules", "dispatch", "tile_prefix", "span")] + [
+        "error", "static_head", "static_next", "rules", "dispatch")] + [
         (name, _I) for name in ("rule_count", "batch_capacity", "max_splits", "max_context",
-                                "kv_heads", "workers", "block_kv", "buckets", "span_units")]
+                                "kv_heads", "workers", "block_kv", "buckets")]
 
 
 class DecodeArgsC(ctypes.Structure):
@@ -35,13 +35,12 @@ class DecodeArgsC(ctypes.Structure):
         "q", "k", "v", "pages", "indptr", "lengths", "request", "split", "begin", "end", "order",
         "offsets", "chunk", "active", "record_count", "mode", "pack_first", "pack_count",
         "num_packs", "counter", "done_counter", "static_head", "static_next", "partial", "lse",
-        "dispatch", "tile_prefix", "span", "edge")] + [
+        "dispatch")] + [
         ("scale", ctypes.c_float), ("_pad0", _I),
         ("q_stride", ctypes.c_int64 * 3), ("k_stride", ctypes.c_int64 * 4),
         ("v_stride", ctypes.c_int64 * 4), ("pt_stride", ctypes.c_int64 * 2)] + [
         (name, _I) for name in ("query_heads", "kv_heads", "head_dim", "max_splits", "page_size",
-                                "csr", "dtype", "workers", "kernel", "dispatch_units",
-                                "batch_capacity", "span_units")]
+                                "csr", "dtype", "workers", "kernel", "dispatch_units")]
 
 
 _SIGNATURES = {
@@ -58,7 +57,6 @@ _SIGNATURES = {
     "sgd_persistent_decode": (_I, [ctypes.POINTER(DecodeArgsC), _P]),
     "sgd_attention_kernel": (_I, [ctypes.POINTER(DecodeArgsC)]),
     "sgd_merge_splits": (_I, [_P] * 6 + [_I] * 5 + [_P]),
-    "sgd_merge_splits_span": (_I, [_P] * 8 + [_I] * 7 + [_P]),
     "sgd_host_static_lists": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "sgd_store_kv_stage_q": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, ctypes.c_int64, _P, _P, _P, _P,
                                   _I, _I, _I, _I, _I, _P]),

@@ -28,9 +28,6 @@ def persistent_decode(plan, layer, q, k, v, pages, indptr, scale, k_strides, v_s
     a.lse = layer.lse.data_ptr()
     if getattr(plan, "dispatch_valid", False):
         a.dispatch, a.dispatch_units = plan.dispatch.data_ptr(), plan.dispatch.shape[0]
-    if getattr(plan, "span_valid", False) and getattr(layer, "edge", None) is not None:
-        a.tile_prefix, a.span, a.edge = plan.tile_prefix.data_ptr(), plan.span.data_ptr(), layer.edge.data_ptr()
-        a.batch_capacity, a.span_units = c.batch_capacity, plan.span_units
     a.scale = float(scale)
     a.q_stride[:] = list(q.stride())
     a.k_stride[:] = list(k_strides)

@@ -3,17 +3,8 @@ from .. import _lib
 from .._lib import check, ptr
 
 
-def merge_splits(plan, layer, span=False):
-    """``span``: the attention ran the span schedule, whose tasks cut by a worker
-    boundary are completed here from the layer's edge states first."""
+def merge_splits(plan, layer):
     c = plan.config
-    if span:
-        check(_lib.lib().sgd_merge_splits_span(
-            ptr(layer.partial), ptr(layer.lse), ptr(plan.counts), ptr(plan.error), ptr(layer.output),
-            ptr(plan.tile_prefix), ptr(plan.chunk), ptr(layer.edge), c.batch_capacity, c.query_heads,
-            c.kv_heads, c.head_dim, c.max_splits, plan.span_units, _lib.dtype_code(layer.output.dtype),
-            _lib.stream_handle(layer.output.device)), "merge_splits_span")
-        return
     check(_lib.lib().sgd_merge_splits(
         ptr(layer.partial), ptr(layer.lse), ptr(plan.counts), ptr(plan.active), ptr(plan.error),
         ptr(layer.output), c.batch_capacity, c.query_heads, c.head_dim, c.max_splits,

@@ -52,15 +52,15 @@ def greedy_lists(plan):
         "greedy_lists")
 
 
-def fused_build(plan, force_mode=-1, run_greedy=False, counters=None, spans=True, csr_metadata=None):
-    """All stages in one launch; optionally clears ``counters`` (int32) in the same launch;
-    ``spans`` also writes the span schedule's tables.  ``csr_metadata`` = (kv_indptr,
+def fused_build(plan, force_mode=-1, run_greedy=False, counters=None, csr_metadata=None):
+    """All stages in one launch; optionally clears ``counters`` (int32) in the same launch.
+    ``csr_metadata`` = (kv_indptr,
     num_kv_splits, batch): the lengths, split counts and active count come from the step's
     CSR metadata inside the launch (and are stored to the plan), instead of from copies
     made into the plan beforehand (integrations/sglang_backend.py:98-99)."""
     n = 0 if counters is None else counters.numel()
     if csr_metadata is None:
-        check(_lib.lib().sgd_build_plan(ctypes.byref(plan.c_struct(spans)), int(force_mode),
+        check(_lib.lib().sgd_build_plan(ctypes.byref(plan.c_struct()), int(force_mode),
                                         int(bool(run_greedy)), ptr(counters), n, _s(plan)), "build_plan")
         return
     indptr, splits, batch = csr_metadata
@@ -71,6 +71,6 @@ def fused_build(plan, force_mode=-1, run_greedy=False, counters=None, spans=True
     if not 0 <= batch <= plan.config.batch_capacity:
         raise ValueError(f"build_plan_csr: batch {batch} outside [0, {plan.config.batch_capacity}]")
     indptr, splits = indptr.contiguous(), splits.contiguous()
-    check(_lib.lib().sgd_build_plan_csr(ctypes.byref(plan.c_struct(spans)), ptr(indptr), ptr(splits), batch,
+    check(_lib.lib().sgd_build_plan_csr(ctypes.byref(plan.c_struct()), ptr(indptr), ptr(splits), batch,
                                         int(force_mode), int(bool(run_greedy)), ptr(counters), n, _s(plan)),
           "build_plan_csr")

@@ -13,19 +13,17 @@ results; used by the parity tests of each stage).
 from ..kernels import plan as K
 
 
-def build_plan(plan, force_mode=-1, *, fused=True, counters=None, spans=False, csr_metadata=None):
-    """``spans``: the fused build also writes the span schedule's tables (only the span
-    kernel reads them).  ``csr_metadata`` = (kv_indptr, num_kv_splits, batch): the fused
+def build_plan(plan, force_mode=-1, *, fused=True, counters=None, csr_metadata=None):
+    """``csr_metadata`` = (kv_indptr, num_kv_splits, batch): the fused
     build reads the step's lengths, split counts and batch from them (no copies into the
     plan beforehand); the staged path makes those copies itself."""
     force_mode = int(force_mode)
     run_greedy = force_mode == 2 or any_static_rule(plan)
     if fused:
-        K.fused_build(plan, force_mode, run_greedy, counters, spans, csr_metadata)
+        K.fused_build(plan, force_mode, run_greedy, counters, csr_metadata)
         plan.dispatch_valid = True
-        plan.span_valid = bool(spans)
         return
-    plan.dispatch_valid = plan.span_valid = False  # the stage launches write neither table
+    plan.dispatch_valid = False  # the stage launches do not write the dispatch table
     if counters is not None:
         counters.zero_()
     if csr_metadata is not None:

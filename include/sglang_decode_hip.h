@@ -35,12 +35,10 @@ enum sgd_dtype { SGD_BF16 = 0, SGD_FP16 = 1 };
 
 /* Attention kernel selection (sgd_decode_args.kernel). */
 enum sgd_kernel {
-    SGD_KERNEL_AUTO = 0,     /* pick by geometry and worker count (see sgd_persistent_decode) */
+    SGD_KERNEL_AUTO = 0,     /* pick by geometry (see sgd_persistent_decode) */
     SGD_KERNEL_GENERIC = 1,  /* any strides/alignment, any supported geometry */
     SGD_KERNEL_VALU = 2,     /* per-task VALU kernel: LDS-staged K/V tiles, DPP reductions, dot2 (group <= 4) */
-    SGD_KERNEL_MFMA = 3,     /* MFMA QK^T and PV, K/V straight from HBM into operands (group 8 or 16) */
-    SGD_KERNEL_STREAM = 4,   /* VALU tile math, one workgroup per CU streaming tiles across tasks (group <= 4) */
-    SGD_KERNEL_SPAN = 5      /* VALU tile math, every wave streams an equal span of the step's tiles (group <= 4) */
+    SGD_KERNEL_MFMA = 3      /* MFMA QK^T and PV, K/V straight from HBM into operands (group <= 16) */
 };
 
 /* Human-readable description of the last SGD_EINVAL / launch failure (thread-local). */
@@ -104,11 +102,8 @@ typedef struct sgd_plan_buffers {
     int32_t *static_head, *static_next;               /* [workers], [T] */
     const int32_t *rules;                             /* [max(rule_count,1)][5] */
     int32_t *dispatch;                                /* optional [T][8] dispatch table, see below; may be NULL */
-    int32_t *tile_prefix, *span;                      /* optional [bcap+1], [span_units][16] span tables, see
-                                                         below; both or neither may be NULL */
     int32_t rule_count;
     int32_t batch_capacity, max_splits, max_context, kv_heads, workers, block_kv, buckets;
-    int32_t span_units;                               /* waves of the span schedule (a multiple of 8) */
 } sgd_plan_buffers;
 
 /*
@@ -121,18 +116,6 @@ typedef struct sgd_plan_buffers {
  * (not for R0); a launch uses an entry only when its kind matches the launch's mode
  * (so a table of an R1 plan serves the STATIC lists installed over it).  The table
  * must come from the same plan build as the other buffers.
- *
- * tile_prefix / span (no reference counterpart): the tables of the span schedule
- * (SGD_KERNEL_SPAN).  The step's work is one sequence of 16-token tiles -- requests
- * in order, then splits, then kv heads, then tiles -- and a request holds
- * ceil(L/16) tiles per kv head.  tile_prefix[r] (r <= bcap) = sum of those counts
- * over rows before r (rows without records count 0).  Wave u of span_units takes
- * tiles [X_u, X_{u+1}) with X_u = floor(u * T / span_units), T = kv_heads *
- * tile_prefix[bcap]; its record span[u][0..15] = {X_u, X_{u+1}, request, split, kv
- * head and tile (within the task) of tile X_u, then that request's tile_prefix,
- * tiles per head, chunk, records and length, 0 x 5} (request = bcap and the rest 0
- * for an empty range).  Written by sgd_build_plan in every mode, forced R0
- * included, when both pointers are set and span_units > 0.
  *
  * Whole plan build in one launch (count/scan, records, order and packs, and,
  * when run_greedy != 0, the STATIC lists).  Same results as the four stage
@@ -200,10 +183,6 @@ typedef struct sgd_decode_args {
     float *partial;                 /* [bcap, Hq, smax, D] */
     float *lse;                     /* [bcap, Hq, smax] */
     const int32_t *dispatch;        /* optional: sgd_build_plan's dispatch table of this plan, or NULL */
-    const int32_t *tile_prefix;     /* span schedule: sgd_build_plan's tile_prefix of this plan, or NULL */
-    const int32_t *span;            /* span schedule: sgd_build_plan's wave records, or NULL */
-    float *edge;                    /* span schedule: [span_units / 8][2][4 heads][D + 2] fp32 scratch for
-                                       the softmax states of tasks cut by a workgroup boundary, or NULL */
     float scale;
     int32_t _pad0;
     int64_t q_stride[3], k_stride[4], v_stride[4], pt_stride[2];
@@ -211,8 +190,6 @@ typedef struct sgd_decode_args {
     int32_t kernel;                 /* enum sgd_kernel */
     int32_t dispatch_units;         /* entries in dispatch; units at or beyond it resolve through
                                        the plan arrays */
-    int32_t batch_capacity;         /* span schedule: rows of the plan (tile_prefix has this + 1) */
-    int32_t span_units;             /* span schedule: the plan's span_units (8 waves per workgroup) */
 } sgd_decode_args;
 
 /*
@@ -246,23 +223,6 @@ int sgd_merge_splits(const float *partial, const float *lse, const int32_t *coun
                      const int32_t *active, const int32_t *error, void *out, int32_t bcap,
                      int32_t query_heads, int32_t head_dim, int32_t max_splits, int32_t dtype,
                      void *stream);
-
-/*
- * Split merge after a span-schedule launch (SGD_KERNEL_SPAN); no reference
- * counterpart (the reference runs every task whole in one program).  A task cut
- * by a workgroup's range left unnormalized softmax states in `edge` (record 1 of
- * the workgroup holding its first tile, record 0 of each later one); they are
- * combined first and written to the task's (request, head, split) slot of
- * partial / lse, so every slot holds its split's normalized partial and LSE as
- * after sgd_merge_splits' inputs, then each row is merged as sgd_merge_splits
- * does.  tile_prefix / chunk / edge / span_units are those of the launch;
- * head_dim 128, group <= 4, partial and edge 16-byte aligned.
- */
-int sgd_merge_splits_span(float *partial, float *lse, const int32_t *counts, const int32_t *error,
-                          void *out, const int32_t *tile_prefix, const int32_t *chunk,
-                          const float *edge, int32_t bcap, int32_t query_heads, int32_t kv_heads,
-                          int32_t head_dim, int32_t max_splits, int32_t span_units, int32_t dtype,
-                          void *stream);
 
 /*
  * The decode step's writes around the attention, one launch per layer.  Replaces the

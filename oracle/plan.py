@@ -144,43 +144,3 @@ def full_plan(lengths, splits, active, cfg, rules=(), force=-1):
                                   e * cfg.kv_heads)
         plan.update(static_head=heads, static_next=nxt)
     return plan
-
-
-def span_tables(lengths, splits, active, cfg, tile=16):
-    """Tables of the span schedule by brute force: the records of count_scan /
-    emit_records (kernels/plan.py:7-45) are expanded into the step's tile sequence
-    (request, then split, then kv head, then the record's ceil((end - begin) / tile)
-    tiles), each tile labelled (request, split, head, tile within the task).
-    tile_prefix[r] counts the per-head tiles of the rows before r.  Wave u of
-    cfg.span_units takes tiles [X_u, X_{u+1}), X_u = floor(u * T / units); its record
-    is [X_u, X_{u+1}, request, split, head, tile of X_u, tile_prefix[request], tiles per
-    head, chunk, records, length, 0 x 5] ([X_u, X_{u+1}, bcap, 0 ...] when empty).
-    No closed form is used, so the kernel's per-request count ceil(L / tile) and its
-    position arithmetic are checked against the records themselves."""
-    bcap, smax = cfg.batch_capacity, cfg.max_splits
-    cs = count_scan(lengths, splits, active, bcap, smax, cfg.max_context)
-    rec = emit_records(lengths, cs["counts"], cs["offsets"], cs["chunk"], bcap, smax, cfg.block_kv,
-                       bcap * smax)
-    label = []  # (request, split, head, tile) of every tile in sequence order
-    prefix = [0] * (bcap + 1)
-    for r in range(bcap):
-        per_head = 0
-        for i in range(cs["offsets"][r], cs["offsets"][r + 1]):
-            nt = -(-(rec["end"][i] - rec["begin"][i]) // tile)
-            per_head += nt
-            for g in range(cfg.kv_heads):
-                label.extend((r, rec["split"][i], g, j) for j in range(nt))
-        prefix[r + 1] = prefix[r] + per_head
-    total = len(label)
-    units = cfg.span_units
-    records = []
-    for u in range(units):
-        x0, x1 = u * total // units, (u + 1) * total // units
-        row = [x0, x1, bcap] + [0] * 13
-        if x0 < x1:
-            r, sp, g, j = label[x0]
-            n = cs["offsets"][r + 1] - cs["offsets"][r]
-            L = lengths[r] if r < len(lengths) else 0
-            row[2:11] = [r, sp, g, j, prefix[r], prefix[r + 1] - prefix[r], cs["chunk"][r], n, L]
-        records.append(row)
-    return dict(tile_prefix=prefix, span=records, tiles=total)

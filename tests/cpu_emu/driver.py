@@ -84,7 +84,7 @@ def from_bits16(a, dtype_code):
 class Plan:
     """PlanBuffers of the executor: same fields, shapes and zero initialization."""
 
-    def __init__(self, emu, config, rules=(), span_units=0):
+    def __init__(self, emu, config, rules=()):
         self.config = c = config
         b, e, t = c.batch_capacity, c.record_capacity, c.task_capacity
         z = lambda n: emu.array((n,), np.int32, 0)
@@ -95,25 +95,19 @@ class Plan:
         self.record_count, self.num_packs, self.mode, self.error = [z(1) for _ in range(4)]
         self.static_head, self.static_next = z(c.workers), z(t)
         self.dispatch = emu.array((t, 8), np.int32, 0)
-        self.span_units = span_units
-        self.tile_prefix = z(b + 1) if span_units else None
-        self.span = emu.array((span_units, 16), np.int32, 0) if span_units else None
         rows = [[r.min_tasks, r.max_tasks, r.min_ratio, r.max_ratio, r.mode] for r in rules]
         self.rules = emu.upload(np.array(rows or [[0, 0, 100, 100, 1]], dtype=np.int32))
         self.rule_count = len(rows)
 
-    def c_struct(self, spans):
+    def c_struct(self):
         c, s = self.config, _lib.PlanBuffersC()
         for name in ("lengths", "splits", "active", "counts", "offsets", "chunk", "request", "split", "begin",
                      "end", "weight", "order", "pack_first", "pack_count", "record_count", "num_packs", "mode",
                      "error", "static_head", "static_next", "rules", "dispatch"):
             setattr(s, name, getattr(self, name).ctypes.data)
-        if spans:
-            s.tile_prefix, s.span = self.tile_prefix.ctypes.data, self.span.ctypes.data
         s.rule_count = self.rule_count
         s.batch_capacity, s.max_splits, s.max_context = c.batch_capacity, c.max_splits, c.max_context
         s.kv_heads, s.workers, s.block_kv, s.buckets = c.kv_heads, c.workers, c.block_kv, c.buckets
-        s.span_units = self.span_units if spans else 0
         return s
 
     def read(self):
@@ -133,8 +127,7 @@ def decode(emu, config, lengths, splits, q, k, v, pages, indptr=None, *, mode=-1
     import torch
     c = config
     dt = _lib.dtype_code(q.dtype)
-    span = kernel == "span"
-    plan = Plan(emu, c, rules, span_units=8 * 256 if span else 0)
+    plan = Plan(emu, c, rules)
     n = len(lengths)
     plan.lengths[:n] = lengths
     plan.splits[:] = 1
@@ -145,10 +138,9 @@ def decode(emu, config, lengths, splits, q, k, v, pages, indptr=None, *, mode=-1
     partial = emu.array((*shape, c.head_dim), np.float32, np.nan if poison else None)
     lse = emu.array(shape, np.float32, np.nan if poison else None)
     out = emu.array((c.batch_capacity, c.query_heads, c.head_dim), np.uint16)
-    edge = emu.array((256, 2, 4 * (c.head_dim + 2)), np.float32) if span else None
     if run_greedy is None:
         run_greedy = int(mode) == 2 or any(int(r.mode) == 2 for r in rules)
-    emu.check(emu.lib.sgd_build_plan(ctypes.byref(plan.c_struct(span)), int(mode), int(bool(run_greedy)),
+    emu.check(emu.lib.sgd_build_plan(ctypes.byref(plan.c_struct()), int(mode), int(bool(run_greedy)),
                                      ptr(sync), 2, None), "build_plan")
     qd, kd, vd = emu.upload(bits16(q)), emu.upload(bits16(k)), emu.upload(bits16(v))
     pd = emu.upload(pages.detach().cpu().numpy().astype(np.int32))
@@ -162,9 +154,6 @@ def decode(emu, config, lengths, splits, q, k, v, pages, indptr=None, *, mode=-1
     a.counter, a.done_counter = sync.ctypes.data, sync[1:].ctypes.data
     a.partial, a.lse = partial.ctypes.data, lse.ctypes.data
     a.dispatch, a.dispatch_units = plan.dispatch.ctypes.data, plan.dispatch.shape[0]
-    if span:
-        a.tile_prefix, a.span, a.edge = plan.tile_prefix.ctypes.data, plan.span.ctypes.data, edge.ctypes.data
-        a.batch_capacity, a.span_units = c.batch_capacity, plan.span_units
     a.scale = float(c.head_dim ** -0.5 if scale is None else scale)
     a.q_stride[:] = list(q.stride())
     if indptr is None:
@@ -180,14 +169,8 @@ def decode(emu, config, lengths, splits, q, k, v, pages, indptr=None, *, mode=-1
     a.kernel = _lib.KERNELS[kernel]
     emu.check(emu.lib.sgd_persistent_decode(ctypes.byref(a), None), "persistent_decode")
     ran = _lib.KERNEL_NAMES[emu.lib.sgd_attention_kernel(ctypes.byref(a))]
-    if span:
-        emu.check(emu.lib.sgd_merge_splits_span(
-            ptr(partial), ptr(lse), ptr(plan.counts), ptr(plan.error), ptr(out), ptr(plan.tile_prefix),
-            ptr(plan.chunk), ptr(edge), c.batch_capacity, c.query_heads, c.kv_heads, c.head_dim, c.max_splits,
-            plan.span_units, dt, None), "merge_splits_span")
-    else:
-        emu.check(emu.lib.sgd_merge_splits(
-            ptr(partial), ptr(lse), ptr(plan.counts), ptr(plan.active), ptr(plan.error), ptr(out),
-            c.batch_capacity, c.query_heads, c.head_dim, c.max_splits, dt, None), "merge_splits")
+    emu.check(emu.lib.sgd_merge_splits(
+        ptr(partial), ptr(lse), ptr(plan.counts), ptr(plan.active), ptr(plan.error), ptr(out),
+        c.batch_capacity, c.query_heads, c.head_dim, c.max_splits, dt, None), "merge_splits")
     return dict(out=from_bits16(out, dt).reshape(out.shape), partial=np.array(partial), lse=np.array(lse),
                 plan=plan.read(), kernel=ran, sync=sync.tolist())

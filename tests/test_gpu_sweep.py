@@ -57,7 +57,7 @@ def kernels_for(c, csr):
     if c.head_dim == 128 and pow2:
         ks.append("mfma")
         if c.group_size <= 4:
-            ks += ["valu", "stream"] + (["span"] if csr else [])
+            ks.append("valu")
     return ks
 
 

@@ -164,24 +164,6 @@ def test_struct_layouts_match_header(tmp_path):
             assert got[(cstruct, name)] == getattr(pystruct, name).offset, (cstruct, name)
 
 
-def test_span_constants_match_layout_header():
-    """The host sizes the span schedule's buffers with the kernel's constants
-    (csrc/span_layout.h): waves per workgroup (edge-state rows = span units / waves),
-    ints per wave record and floats per edge state."""
-    import re
-    from sglang_decode import config
-    text = open(os.path.join(ROOT, "-sglang-decode-_amd", "csrc", "span_layout.h")).read()
-    const = {m.group(1): int(m.group(2)) for m in re.finditer(r"constexpr int (k\w+) = (\d+);", text)}
-    assert config.SPAN_WAVES_PER_WORKGROUP == const["kWaves"]
-    assert config.span_workgroups(config.span_units("cpu")) * const["kWaves"] == config.span_units("cpu")
-    assert const["kRecord"] == 16  # runtime/workspace.py: span = ints(units * 16)
-    import torch
-    from sglang_decode.runtime.workspace import LayerBuffers
-    layer = LayerBuffers.allocate(config.DecodeConfig(), "cpu", torch.bfloat16)
-    assert tuple(layer.edge.shape) == (config.span_workgroups(config.span_units("cpu")), 2,
-                                       const["kHeads"] * const["kD"] + 2 * const["kHeads"])
-
-
 def test_host_static_lists_cpp_matches_reference(plan_vectors):
     from sglang_decode import _lib
     lib = _lib.lib()
@@ -223,21 +205,23 @@ def test_attention_kernel_selection_is_host_only():
     args.max_splits, args.page_size, args.csr, args.workers = 16, 1, 1, 256
     args.k_stride[:] = [1024, 0, 128, 1]
     args.v_stride[:] = [1024, 0, 128, 1]
-    for forced in ("generic", "valu", "stream", "mfma"):
+    for forced in ("generic", "valu", "mfma"):
         args.kernel = _lib.KERNELS[forced]
         assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == forced
-    args.query_heads = 64  # group 8: no VALU / stream kernel, the MFMA one serves it
-    for forced in ("valu", "stream"):
-        args.kernel = _lib.KERNELS[forced]
-        assert lib.sgd_attention_kernel(ctypes.byref(args)) == -22
-        assert b"group <= 4" in lib.sgd_last_error()
+    # AUTO picks a bitwise-repeatable kernel whatever the worker count: VALU for group 4
+    # with one worker per CU (the reference's convention) as with two
+    args.kernel = _lib.KERNELS["auto"]
+    for workers in (108, 256, 512):
+        args.workers = workers
+        assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "valu"
+    args.query_heads = 64  # group 8: no VALU kernel, the MFMA one serves it
+    assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "mfma"
+    args.kernel = _lib.KERNELS["valu"]
+    assert lib.sgd_attention_kernel(ctypes.byref(args)) == -22
+    assert b"group <= 4" in lib.sgd_last_error()
     args.kernel = _lib.KERNELS["mfma"]
     assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "mfma"
     args.head_dim = 64  # head_dim 64: only the generic kernel
-    assert lib.sgd_attention_kernel(ctypes.byref(args)) == -22
-    args.kernel, args.head_dim = _lib.KERNELS["auto"], 128
-    args.query_heads, args.kernel = 32, _lib.KERNELS["stream"]
-    args.partial = (1 << 20) + 4  # the stream kernel stores partial rows 16 bytes at a time
     assert lib.sgd_attention_kernel(ctypes.byref(args)) == -22
 
 

@@ -295,37 +295,3 @@ def test_merge_of_split_partials_equals_unsplit_attention():
     flat = np.where(np.isnan(lse), lse, 0.0).astype(np.float32)
     assert not np.allclose(OP.merge_splits(partial, flat, cs["counts"], 0, 3, hq, d, 4)[0], direct[0],
                            atol=1e-3)
-
-
-def test_span_tables_hand_case():
-    """lengths [0, 1, 33, 513] with splits [16, 16, 16, 2] (the tail case of
-    tests/unit/test_planning.py:29-33): records per request 0, 1, 2, 2 with spans
-    (0,32) | (0,32),(32,33) | (0,288),(288,513), so per-head tiles 0, 1, 2+1, 18+15 and
-    tile_prefix [0, 0, 1, 4, 37].  With 2 kv heads T = 74 (request 1: tiles 0-1,
-    request 2: 2-7, request 3: 8-73); 3 waves start at tiles 0, 24, 49: request 1 split 0
-    head 0 tile 0; request 3 split 0 head 0 tile 16 (24 - 8); request 3 split 1 head 0
-    tile 5 (49 - 8 - 2 * 18)."""
-    cfg = types.SimpleNamespace(batch_capacity=4, max_splits=16, max_context=1024, span_units=3,
-                                kv_heads=2, block_kv=128)
-    got = OP.span_tables([0, 1, 33, 513], [16, 16, 16, 2], 4, cfg)
-    assert got["tile_prefix"] == [0, 0, 1, 4, 37]
-    assert got["tiles"] == 74
-    assert [row[:6] for row in got["span"]] == [[0, 24, 1, 0, 0, 0], [24, 49, 3, 0, 0, 16],
-                                                [49, 74, 3, 1, 0, 5]]
-    assert got["span"][1][6:11] == [4, 33, 288, 2, 513]
-
-
-@pytest.mark.parametrize("seed", range(4))
-def test_span_tables_per_request_count(seed):
-    """Whatever the splits, a request's per-head tiles equal ceil(L / 16): the splits
-    are multiples of 32 tokens except the last (kernels/plan.py:18)."""
-    rng = np.random.default_rng(seed)
-    bcap = 12
-    lengths = [int(x) for x in rng.integers(0, 3000, size=bcap)]
-    splits = [int(x) for x in rng.integers(1, 17, size=bcap)]
-    cfg = types.SimpleNamespace(batch_capacity=bcap, max_splits=16, max_context=4096, span_units=7,
-                                kv_heads=8, block_kv=128)
-    got = OP.span_tables(lengths, splits, 9, cfg)
-    for r in range(bcap):
-        expect = -(-lengths[r] // 16) if r < 9 else 0
-        assert got["tile_prefix"][r + 1] - got["tile_prefix"][r] == expect
