@@ -43,6 +43,15 @@ class DecodeArgsC(ctypes.Structure):
                                 "csr", "dtype", "workers", "kernel", "dispatch_units")]
 
 
+class NoAllocArgsC(ctypes.Structure):
+    _fields_ = [(name, _P) for name in ("q", "k", "v", "pages", "indptr", "lengths", "splits", "active", "out")] + [
+        ("scale", ctypes.c_float), ("_pad0", _I),
+        ("q_stride", ctypes.c_int64 * 3), ("k_stride", ctypes.c_int64 * 4),
+        ("v_stride", ctypes.c_int64 * 4), ("pt_stride", ctypes.c_int64 * 2)] + [
+        (name, _I) for name in ("batch_capacity", "max_splits", "max_context", "query_heads", "kv_heads",
+                                "head_dim", "page_size", "csr", "dtype", "workers", "force_mode", "kernel")]
+
+
 _SIGNATURES = {
     "sgd_last_error": (ctypes.c_char_p, []),
     "sgd_version": (ctypes.c_char_p, []),
@@ -58,6 +67,7 @@ _SIGNATURES = {
     "sgd_attention_kernel": (_I, [ctypes.POINTER(DecodeArgsC)]),
     "sgd_merge_splits": (_I, [_P] * 6 + [_I] * 5 + [_P]),
     "sgd_host_static_lists": (_I, [_P, _I, _I, _I, _I, _P, _P]),
+    "sgd_decode_noalloc": (_I, [ctypes.POINTER(NoAllocArgsC), _P]),
     "sgd_store_kv_stage_q": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, ctypes.c_int64, _P, _P, _P, _P,
                                   _I, _I, _I, _I, _I, _P]),
 }

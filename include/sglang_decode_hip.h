@@ -255,6 +255,38 @@ int sgd_host_static_lists(const int32_t *weight, int32_t record_count, int32_t k
                           int32_t workers, int32_t task_capacity, int32_t *static_head,
                           int32_t *static_next);
 
+/* Arguments of sgd_decode_noalloc: the inputs of one decode step and its output. */
+typedef struct sgd_noalloc_args {
+    const void *q, *k, *v;          /* as in sgd_decode_args */
+    const int32_t *pages;           /* paged: table [bcap, max_pages]; CSR: kv_indices */
+    const int32_t *indptr;          /* CSR: kv_indptr [bcap+1]; NULL when paged */
+    const int32_t *lengths, *splits;/* plan inputs [bcap] (as sgd_plan_buffers.lengths / .splits) */
+    const int32_t *active;          /* [1] active rows */
+    void *out;                      /* [bcap, Hq, D] in `dtype`, contiguous */
+    float scale;
+    int32_t _pad0;
+    int64_t q_stride[3], k_stride[4], v_stride[4], pt_stride[2];
+    int32_t batch_capacity, max_splits, max_context, query_heads, kv_heads, head_dim, page_size, csr, dtype,
+        workers;
+    int32_t force_mode;             /* -1 (R1: no policy rules) or a Mode id to force */
+    int32_t kernel;                 /* enum sgd_kernel */
+} sgd_noalloc_args;
+
+/*
+ * One decode step that allocates nothing: sgd_build_plan (no policy rules, block_kv
+ * 128), sgd_persistent_decode and sgd_merge_splits on `stream`, with the plan and
+ * dispatch tables, the claim counters and the split partial/LSE slots in a static
+ * device array of 32 MiB held by the library on every GPU it runs on.  No counterpart
+ * in the reference: for callers that cannot call hipMalloc (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation); the caller passes
+ * only the inputs and `out`.  Geometries whose buffers exceed the array (batch_capacity
+ * x max_splits x Hq x head_dim x 4 bytes of split slots, plus the tables) return
+ * SGD_EINVAL with the size needed.  The first call on a device looks up the array's
+ * address there (make it outside graph capture).  Every call on one GPU reuses that
+ * GPU's array: calls that overlap on one GPU race.
+ */
+int sgd_decode_noalloc(const sgd_noalloc_args *args, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

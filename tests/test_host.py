@@ -138,16 +138,18 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layouts_match_header(tmp_path):
     """Every ctypes field sits at the offset the C header gives it (gcc prints offsetof
-    for each field of sgd_decode_args and sgd_plan_buffers), and the sizes agree."""
+    for each field of sgd_decode_args, sgd_plan_buffers and sgd_noalloc_args), and the sizes
+    agree."""
     import shutil
     import subprocess
-    from sglang_decode._lib import DecodeArgsC, PlanBuffersC
+    from sglang_decode._lib import DecodeArgsC, NoAllocArgsC, PlanBuffersC
     gcc = shutil.which("gcc")
     if gcc is None:
         pytest.skip("gcc not available")
     include = os.path.join(ROOT, "include")
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "sglang_decode_hip.h"', 'int main(void) {']
-    for cstruct, pystruct in (("sgd_decode_args", DecodeArgsC), ("sgd_plan_buffers", PlanBuffersC)):
+    for cstruct, pystruct in (("sgd_decode_args", DecodeArgsC), ("sgd_plan_buffers", PlanBuffersC),
+                              ("sgd_noalloc_args", NoAllocArgsC)):
         lines.append(f'printf("{cstruct} size %zu\\n", sizeof({cstruct}));')
         for name, _ in pystruct._fields_:
             lines.append(f'printf("{cstruct} {name} %zu\\n", offsetof({cstruct}, {name}));')
@@ -158,7 +160,8 @@ def test_struct_layouts_match_header(tmp_path):
     subprocess.run([gcc, "-I", include, str(src), "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
     got = {tuple(line.split()[:2]): int(line.split()[2]) for line in out if line}
-    for cstruct, pystruct in (("sgd_decode_args", DecodeArgsC), ("sgd_plan_buffers", PlanBuffersC)):
+    for cstruct, pystruct in (("sgd_decode_args", DecodeArgsC), ("sgd_plan_buffers", PlanBuffersC),
+                              ("sgd_noalloc_args", NoAllocArgsC)):
         assert got[(cstruct, "size")] == ctypes.sizeof(pystruct), cstruct
         for name, _ in pystruct._fields_:
             assert got[(cstruct, name)] == getattr(pystruct, name).offset, (cstruct, name)
@@ -274,3 +277,22 @@ def test_host_static_schedule_installs_reference_lists(plan_vectors):
     assert engine.plan.mode.item() == 2
     with pytest.raises(ValueError):  # capacities are checked on the host
         hs.plan_lists([c.max_context + 1], [1])
+
+
+def test_noalloc_rejects_geometry_beyond_its_scratch_before_any_device_call():
+    """sgd_decode_noalloc's buffers must fit the library's 32 MiB array: batch 128 x 64
+    splits x 32 heads x 128 dims of fp32 split slots (134 MB) is refused with the size
+    needed, before the device is touched (this host has no GPU)."""
+    from sglang_decode import _lib
+    lib = _lib.lib()
+    a = _lib.NoAllocArgsC()
+    for name in ("q", "k", "v", "pages", "indptr", "lengths", "splits", "active", "out"):
+        setattr(a, name, 1 << 20)
+    a.batch_capacity, a.max_splits, a.max_context, a.workers = 128, 64, 32768, 512
+    a.query_heads, a.kv_heads, a.head_dim, a.page_size, a.csr = 32, 8, 128, 1, 1
+    assert lib.sgd_decode_noalloc(ctypes.byref(a), None) == -22
+    msg = lib.sgd_last_error()
+    assert b"needs" in msg and b"33554432" in msg
+    a.out = None
+    assert lib.sgd_decode_noalloc(ctypes.byref(a), None) == -22
+    assert b"null buffer" in lib.sgd_last_error()
