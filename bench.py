@@ -15,20 +15,23 @@ splits), `--workload c4` the Llama-3-70B paged layer (page 16, 64 q / 8 kv, batc
 c5` the 32-layer step of the 8B shape at batch 64 (contexts lognormal, median 2048)
 with a 256k-token pool per layer.
 
-Reported per schedule (R1, STATIC, STATIC_HOST, D1, D4, R0): us/layer = replay time /
-layers, achieved GB/s = algorithmic bytes per layer / us/layer.  STATIC builds its LPT
-lists on the device inside the replay (the reference's device greedy, a serial
-chain); STATIC_HOST is the reference benchmark's host-static variant
-(benchmarks/bench_decode.py:14-30): C++ heap LPT on the host when the lengths change,
-lists installed after the device R1 plan.  `value` is the achieved HBM GB/s of the
-fastest schedule.  `roofline` times the attention kernel alone for that schedule: a
-HIP graph of back-to-back launches (rotating layers) replayed between HIP events on
-its stream.
+Reported per schedule (R1, STATIC, STATIC_HOST, D1, D4, R0), timed in 5 alternating
+rounds as the reference's benchmark does (benchmarks/bench_decode.py:76-91): us/layer =
+replay time / layers, achieved GB/s = algorithmic bytes per layer / us/layer, and an
+oracle check (layer 0 within 2e-2 abs / 1e-2 rel of the FP32 oracle, and every layer that
+reads the same pool bitwise equal to it).  STATIC builds its LPT lists on the device
+inside the replay (the reference's device greedy, a serial chain); STATIC_HOST is the
+reference benchmark's host-static variant (benchmarks/bench_decode.py:14-30): C++ heap
+LPT on the host when the lengths change, uploaded from pinned memory, installed after
+the device R1 plan.  `value` is the achieved HBM GB/s of the fastest schedule.
+`roofline` times the attention kernel alone for that schedule: a HIP graph of
+back-to-back launches (rotating layers) replayed between HIP events on its stream.
 `attention_merge_us` (attention + merge per layer, no plan) and `single_layer_entry_us`
-(one layer's full entry: plan build + attention + merge, the reference's
-benchmarks/bench_decode.py:94 boundary) are timed the same way for that schedule.
-`cpu_baseline` is the FP32 oracle on the same inputs, timed on this host (bounded
-sample stated in the record).
+(one layer's full entry: plan build + attention + merge) are timed the same way for that
+schedule; `entry` times that full entry per schedule at the reference's own boundary:
+eager calls, GPU time and host wall time per call, STATIC_HOST re-planning on the host
+and uploading on every call.  `cpu_baseline` is the FP32 oracle on the same inputs on
+every host core, and the CPU planning spec, timed on this host (1 warmup, median of 5).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--workload c2]
 """
@@ -79,7 +82,11 @@ def parse():
     ap.add_argument("--kv-store", action="store_true",
                     help="also time the decode step's KV-pool write + q staging: one launch "
                          "(kernels/kv_store.py) against upstream's two scatters and a copy")
-    ap.add_argument("--rounds", type=int, default=3, help="timed rounds per schedule (median reported)")
+    ap.add_argument("--rounds", type=int, default=5,
+                    help="alternating timed rounds per schedule (median reported)")
+    ap.add_argument("--entry-iterations", type=int, default=200,
+                    help="eager single-layer full-entry calls per round and schedule (the reference "
+                         "benchmark's boundary, STATIC_HOST planning on the host every call); 0 skips")
     ap.add_argument("--samples-csv", default="",
                     help="write one row per schedule and round (variant, trial, iterations, gpu_us, wall_us, "
                          "status: per step of all layers) for planning.calibrate")
@@ -284,18 +291,43 @@ def main():
     bytes_per_layer = W.algorithmic_bytes(lengths, c)
     torch.cuda.synchronize()
 
-    results = {}
-    engines = {}
-    samples = []
+    # the oracle's view of pool 0 (the pool of layer 0), gathered to the host once, outside
+    # any timed region: the used KV rows or pages, relabelled, with q -- a paged layout
+    # for the threaded CPU oracle (CSR rows are pages of one token)
+    from oracle import attention as OA
+    x = fx[0]
+    if csr:
+        idx = x[4].long()
+        rows_k, rows_v = x[1][idx].cpu()[:, None], x[2][idx].cpu()[:, None]
+        table = torch.zeros((batch, max(lengths)), dtype=torch.int32)
+        starts = x[3][:batch].cpu().tolist()
+        for r, n in enumerate(lengths):
+            table[r, :n] = torch.arange(starts[r], starts[r] + n, dtype=torch.int32)
+        host = (x[0][:batch].cpu(), rows_k, rows_v, table, 1)
+    else:
+        used = [x[3][r, :(n + c.page_size - 1) // c.page_size].long() for r, n in enumerate(lengths)]
+        flat = torch.cat(used)
+        table = torch.full((batch, c.max_pages), -1, dtype=torch.int32)
+        cursor = 0
+        for r, u in enumerate(used):
+            table[r, :u.numel()] = torch.arange(cursor, cursor + u.numel(), dtype=torch.int32)
+            cursor += u.numel()
+        host = (x[0][:batch].cpu(), x[1][flat].cpu(), x[2][flat].cpu(), table, c.page_size)
+    cpu_threads = len(os.sched_getaffinity(0))
+    oracle = lambda: OA.paged_attention_threads(*host[:4], lengths, host[4], threads=cpu_threads)[:batch]
+    expected = None if args.no_check and args.no_cpu_baseline else oracle()
+
+    engines, hosts, samples = {}, {}, []
     host_lpt_us = None
     for name in [p for p in args.policies.split(",") if p]:
         host_static = name == "STATIC_HOST"
         mode = int(Mode.R1 if host_static else Mode[name])
         engine = DecodeEngine(c, device=dev, dtype=dtype, layers=layers, force_mode=mode, kernel=args.kernel)
         if host_static:
-            hs = HostStatic(engine)
+            hs = hosts[name] = HostStatic(engine)
             t0 = time.perf_counter()
             hs.plan_lists(lengths, splits)
+            torch.cuda.synchronize()
             host_lpt_us = (time.perf_counter() - t0) * 1e6
             device_prepare = engine.prepare
 
@@ -309,9 +341,15 @@ def main():
         graph.capture()
         for _ in range(args.warmup):
             graph.replay()
-        torch.cuda.synchronize()
-        rounds = []
-        for trial in range(args.rounds):
+        engines[name] = (engine, graph)
+    torch.cuda.synchronize()
+
+    # alternating rounds (benchmarks/bench_decode.py:76-91): the schedules in order on even
+    # rounds, reversed on odd ones; per round the mean of `steps` replays
+    rounds = {name: [] for name in engines}
+    for trial in range(args.rounds):
+        for name in (list(engines) if trial % 2 == 0 else list(reversed(engines))):
+            graph = engines[name][1]
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
             wall0 = time.perf_counter_ns()
@@ -320,17 +358,18 @@ def main():
                 graph.replay()
             end.record()
             end.synchronize()
-            rounds.append(start.elapsed_time(end) / args.steps)
+            rounds[name].append(start.elapsed_time(end) / args.steps)
             # STATIC_HOST is the reference benchmark's STATIC_CPU variant
-            samples.append(dict(variant="STATIC_CPU" if host_static else name, trial=trial, iterations=args.steps,
-                                gpu_us=round(rounds[-1] * 1000.0, 3),
+            samples.append(dict(variant="STATIC_CPU" if name == "STATIC_HOST" else name, trial=trial,
+                                iterations=args.steps, gpu_us=round(rounds[name][-1] * 1000.0, 3),
                                 wall_us=round((time.perf_counter_ns() - wall0) / 1000.0 / args.steps, 3),
                                 status="ok"))
-        ms_step = statistics.median(rounds)
+    results = {}
+    for name, (engine, graph) in engines.items():
+        ms_step = statistics.median(rounds[name])
         us_layer = ms_step * 1000.0 / layers
         results[name] = dict(ms_per_step=ms_step, us_per_layer=us_layer,
                              gbps=bytes_per_layer / (us_layer * 1e-6) / 1e9)
-        engines[name] = (engine, graph)
         print(f"[bench] {name}: {us_layer:.2f} us/layer  {results[name]['gbps']:.0f} GB/s "
               f"({100 * results[name]['gbps'] / PEAK_HBM_GBS:.1f}% of peak)", flush=True)
 
@@ -340,44 +379,29 @@ def main():
             w = csv.DictWriter(f, fieldnames=["variant", "trial", "iterations", "gpu_us", "wall_us", "status"])
             w.writeheader()
             w.writerows(samples)
+
+    # every reported schedule against the FP32 oracle: after one more replay, every layer
+    # that reads pool 0 (layers 0, pools, 2 * pools, ...) must equal layer 0 bit for bit,
+    # and layer 0 must be within 2e-2 abs / 1e-2 rel of the oracle
+    check = None
+    if not args.no_check:
+        check, failed = {}, []
+        for name, (engine, graph) in engines.items():
+            graph.replay()
+            torch.cuda.synchronize()
+            out0 = engine.layers[0].output[:batch]
+            same = all(torch.equal(engine.layers[li].output[:batch], out0) for li in range(0, layers, pools))
+            out = out0.float().cpu().numpy()
+            ok = bool(np.allclose(out, expected, atol=2e-2, rtol=1e-2)) and same
+            check[name] = dict(ok=ok, max_abs_err=round(float(np.max(np.abs(out - expected))), 6))
+            if not ok:
+                failed.append(name)
+        print(f"[bench] oracle check: {check}", flush=True)
+        if failed:
+            print(f"[bench] OUTPUT MISMATCH against the oracle: {failed}", file=sys.stderr)
+            sys.exit(3)
     best = min(results, key=lambda k: results[k]["us_per_layer"])
     engine, graph = engines[best]
-
-    # correctness of the reported schedule: layer 0 against the FP32 oracle.  The used KV
-    # rows / pages are gathered to the host first (outside any timed region).
-    from oracle import attention as OA
-    x = fx[0]
-    if csr:
-        idx = x[4].long()
-        host = (x[0].cpu(), x[1][idx].cpu(), x[2][idx].cpu(), x[3].cpu(),
-                torch.arange(idx.numel(), dtype=torch.int32))
-        oracle = lambda: OA.csr_attention(*host, lengths)[:batch]
-    else:
-        used = [x[3][r, :(n + c.page_size - 1) // c.page_size].long() for r, n in enumerate(lengths)]
-        flat = torch.cat(used)
-        table = torch.full((batch, c.max_pages), -1, dtype=torch.int32)
-        cursor = 0
-        for r, u in enumerate(used):
-            table[r, :u.numel()] = torch.arange(cursor, cursor + u.numel(), dtype=torch.int32)
-            cursor += u.numel()
-        host = (x[0][:batch].cpu(), x[1][flat].cpu(), x[2][flat].cpu(), table)
-        oracle = lambda: OA.paged_attention(*host, lengths, c.page_size)[:batch]
-    check, cpu_times, expected = None, [], None
-    if not (args.no_check and args.no_cpu_baseline):
-        t0 = time.perf_counter()
-        expected = oracle()
-        cpu_times.append(time.perf_counter() - t0)
-    if not args.no_check:
-        graph.replay()
-        torch.cuda.synchronize()
-        out = engine.layers[0].output[:batch].float().cpu().numpy()
-        ok = bool(np.allclose(out, expected, atol=2e-2, rtol=1e-2))
-        check = dict(ok=ok, max_abs_err=float(np.max(np.abs(out - expected))))
-        print(f"[bench] oracle check ({best}): ok={ok} max_abs_err={check['max_abs_err']:.4g}",
-              flush=True)
-        if not ok:
-            print("[bench] OUTPUT MISMATCH against the oracle", file=sys.stderr)
-            sys.exit(3)
 
     # roofline: the attention kernel alone, a batch of launches back to back (rotating
     # layers) captured in a HIP graph and replayed between two HIP events on its stream,
@@ -474,19 +498,74 @@ def main():
         torch.cuda.synchronize()
         print(f"[bench] copy calibration: 5 x {args.copy_calibration_mib} MiB read+write", flush=True)
 
+    # the reference's benchmark boundary (benchmarks/bench_decode.py:44-91): eager single-layer
+    # full-entry calls -- plan + attention + merge, STATIC_HOST also planning its LPT lists
+    # on the host and uploading them on every call -- in alternating rounds; GPU time from
+    # HIP events and host wall time per call, medians over the rounds
+    entry = {}
+    if args.entry_iterations > 0:
+        calls = {}
+        for name, (eng, gr) in engines.items():
+            def call(name=name, eng=eng, gr=gr):
+                if name == "STATIC_HOST":
+                    hosts[name].prepare(lengths, splits)
+                else:
+                    eng.prepare()
+                eng.execute(gr.q[0], *gr.kv_pairs[0], gr.pages[0], layer=0, indptr=gr.indptr[0])
+            for _ in range(max(1, args.entry_iterations // 10)):
+                call()
+            calls[name] = call
+        torch.cuda.synchronize()
+        rows = {name: ([], []) for name in calls}
+        for trial in range(args.rounds):
+            for name in (list(calls) if trial % 2 == 0 else list(reversed(calls))):
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                wall0 = time.perf_counter_ns()
+                start.record()
+                for _ in range(args.entry_iterations):
+                    calls[name]()
+                end.record()
+                end.synchronize()
+                rows[name][0].append(start.elapsed_time(end) * 1000.0 / args.entry_iterations)
+                rows[name][1].append((time.perf_counter_ns() - wall0) / 1000.0 / args.entry_iterations)
+        entry = {name: dict(gpu_us=round(statistics.median(g), 2), wall_us=round(statistics.median(w), 2))
+                 for name, (g, w) in rows.items()}
+        print(f"[bench] single-layer full entry per call (eager, reference boundary): {entry}", flush=True)
+
     cpu = None
     if not args.no_cpu_baseline:
-        # the sample: the full layer (all requests) on host-resident fp32-upcast inputs
-        for _ in range(2):
-            t0 = time.perf_counter()
-            oracle()
-            cpu_times.append(time.perf_counter() - t0)
-        t = statistics.median(cpu_times)
-        cpu = dict(value=round(t * 1e6, 1), unit="us/layer", cores=1, kind="port",
-                   sample=f"FP32 numpy oracle over the full layer ({batch} requests, "
-                          f"{sum(lengths)} context tokens), median of 3, single thread",
-                   tokens_per_s=round(batch / t, 2), kv_tokens_per_s=round(sum(lengths) / t, 1))
-        print(f"[bench] cpu baseline: {t * 1e3:.1f} ms/layer", flush=True)
+        # the FP32 oracle over the full layer (every request) on every host core, and the CPU
+        # planning spec (split_records -> bucket_order -> make_packs -> greedy_static) on the
+        # same lengths: 1 warmup, then the median of 5 runs each
+        from sglang_decode.planning import reference as R
+
+        def cpu_plan():
+            recs, _, _ = R.split_records(lengths, splits, c)
+            R.make_packs(recs, R.bucket_order(recs), c.kv_heads, c.workers)
+            R.greedy_static(recs, c.kv_heads, c.workers)
+
+        def median_of(fn, runs=5):
+            fn()
+            times = []
+            for _ in range(runs):
+                t0 = time.perf_counter()
+                fn()
+                times.append(time.perf_counter() - t0)
+            return statistics.median(times)
+
+        t = median_of(oracle)
+        plan_t = median_of(cpu_plan)
+        cpu = dict(value=round(t * 1e6, 1), unit="us/layer", cores=cpu_threads, kind="port", runs=5, warmup=1,
+                   sample=f"FP32 oracle (reference/attention.py:5-18 restated in torch CPU fp32) over the full "
+                          f"layer ({batch} requests, {sum(lengths)} context tokens) on {cpu_threads} host threads, "
+                          f"median of 5 after 1 warmup",
+                   tokens_per_s=round(batch / t, 2), kv_tokens_per_s=round(sum(lengths) / t, 1),
+                   plan_us=round(plan_t * 1e6, 1),
+                   plan_sample="CPU planning spec (split_records, bucket_order, make_packs, greedy_static) on the "
+                               "same lengths, one thread, median of 5 after 1 warmup")
+        print(f"[bench] cpu baseline: {t * 1e3:.1f} ms/layer on {cpu_threads} threads; planning spec "
+              f"{plan_t * 1e6:.0f} us", flush=True)
 
     r = results[best]
     line = {
@@ -509,6 +588,7 @@ def main():
         "cpu_baseline": cpu,
         "attention_merge_us": round(attn_merge_us, 2),
         "single_layer_entry_us": round(single_layer_us, 2),
+        "entry": entry,
     }
     if kv_store is not None:
         line["kv_store"] = kv_store

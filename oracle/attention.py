@@ -63,6 +63,45 @@ def paged_attention(q, k, v, pages, lengths, page_size, scale=None):
     return out
 
 
+def paged_attention_threads(q, k, v, pages, lengths, page_size, scale=None, threads=1):
+    """paged_attention with the requests spread over `threads` host threads, for timing
+    the CPU baseline on every core: per request (longest first) the rows are gathered
+    in their storage dtype and upcast to float32, each KV head repeated for its group,
+    then softmax(q.k * scale) @ v -- reference/attention.py:5-18 step for step, in torch
+    CPU float32 (its ops release the GIL; one intra-op thread per worker thread).
+    q/k/v/pages: CPU tensors or arrays of the shapes of paged_attention."""
+    import concurrent.futures
+
+    import torch
+    q, k, v = (x if isinstance(x, torch.Tensor) else torch.from_numpy(np.asarray(x)) for x in (q, k, v))
+    pages = torch.as_tensor(_ints(pages))
+    d = q.shape[-1]
+    scale = d ** -0.5 if scale is None else float(scale)
+    group = q.shape[1] // k.shape[2]
+    out = torch.zeros(q.shape, dtype=torch.float32)
+
+    def one(r):
+        n = int(lengths[r])
+        if n == 0:
+            return
+        token = torch.arange(n)
+        phys, inner = pages[r, token // page_size], token % page_size
+        key = k[phys, inner].float().repeat_interleave(group, dim=1)    # [L, Hq, D]
+        value = v[phys, inner].float().repeat_interleave(group, dim=1)
+        score = torch.einsum("hd,thd->ht", q[r].float(), key) * scale
+        out[r] = torch.einsum("ht,thd->hd", torch.softmax(score, dim=-1), value)
+
+    order = sorted(range(len(lengths)), key=lambda r: -int(lengths[r]))
+    previous = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        with concurrent.futures.ThreadPoolExecutor(max(1, int(threads))) as pool:
+            list(pool.map(one, order))
+    finally:
+        torch.set_num_threads(previous)
+    return out.numpy()
+
+
 def csr_attention(q, k, v, kv_indptr, kv_indices, lengths, scale=None):
     """CSR token-index form (page_size 1): k/v [tokens, Hkv, D]."""
     k, v = _f32(k), _f32(v)

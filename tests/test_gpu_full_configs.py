@@ -80,3 +80,28 @@ def test_skewed_batch128_every_request(mode):
 def test_llama70b_paged_batch32_every_request(mode, dtype):
     engine = check("c4", mode, dtype)
     assert engine.attention_kernel_name() == "mfma"
+
+
+def test_llama8b_batch64_host_static_every_request():
+    """STATIC_HOST at the reference benchmark's boundary (benchmarks/bench_decode.py:14-30):
+    the host LPT lists uploaded from pinned memory over the R1 plan, on every request of
+    the batch-64 layer, twice in a row (the second call re-plans into the same staging
+    buffers).  The installed lists equal the planning spec's, the mode is STATIC, and the
+    output is within tolerance of the FP32 oracle."""
+    from sglang_decode.planning.host_static import HostStatic
+    from sglang_decode.planning.reference import greedy_static, lists_to_links
+    c, lengths, splits, inputs, indptr, expected = workload("c2")
+    engine = DecodeEngine(c, force_mode=Mode.R1)
+    W.update_plan(engine, lengths, splits)
+    hs = HostStatic(engine)
+    records, _, _ = split_records(lengths, splits, c)
+    heads, links = lists_to_links(greedy_static(records, c.kv_heads, c.workers), c.workers, c.task_capacity)
+    for _ in range(2):
+        engine.layers[0].partial.fill_(float("nan"))
+        hs.prepare(lengths, splits)
+        out = engine.execute(*inputs, indptr=indptr)
+        torch.cuda.synchronize()
+        assert engine.plan.mode.item() == int(Mode.STATIC)
+        assert engine.plan.static_head.tolist() == heads
+        assert engine.plan.static_next.tolist() == links
+        close(out[:len(lengths)], expected[:len(lengths)], msg="c2 STATIC_HOST")

@@ -295,3 +295,20 @@ def test_merge_of_split_partials_equals_unsplit_attention():
     flat = np.where(np.isnan(lse), lse, 0.0).astype(np.float32)
     assert not np.allclose(OP.merge_splits(partial, flat, cs["counts"], 0, 3, hq, d, 4)[0], direct[0],
                            atol=1e-3)
+
+
+def test_threaded_oracle_matches_serial_oracle():
+    """The CPU baseline's threaded restatement (every host core) computes what the serial
+    oracle does: same gather, upcast and softmax, to float32 rounding."""
+    import torch
+    gen = torch.Generator().manual_seed(5)
+    b, hq, hkv, d, page = 6, 8, 2, 128, 16
+    lengths = [0, 1, 37, 130, 64, 5]
+    pages = torch.randperm(60, generator=gen)[:b * 10].view(b, 10).to(torch.int32)
+    q = torch.randn((b, hq, d), generator=gen).to(torch.bfloat16)
+    k = torch.randn((60, page, hkv, d), generator=gen).to(torch.bfloat16)
+    v = torch.randn((60, page, hkv, d), generator=gen).to(torch.bfloat16)
+    serial = OA.paged_attention(q, k, v, pages, lengths, page)
+    threaded = OA.paged_attention_threads(q, k, v, pages, lengths, page, threads=3)
+    np.testing.assert_allclose(threaded, serial, rtol=1e-5, atol=1e-5)
+    assert not threaded[0].any()
