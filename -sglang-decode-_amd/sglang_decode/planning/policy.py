@@ -1,9 +1,11 @@
-"""Offline policy loading.  Uncalibrated workloads default to direct round robin.
+"""Policy files: which schedule the device plan picks for a batch's shape.
 
-Same contract as src/sglang_decode/planning/policy.py:7-28: a policy file is JSON
-``{"status": "validated", "evidence": [...], "rules": [{min_tasks, max_tasks,
-min_ratio, max_ratio, mode}, ...]}``; anything not explicitly validated, or
-carrying no evidence, is rejected, and only R1/STATIC/D1/D4 may be selected.
+A policy file is the JSON artifact of the calibration gate (planning/calibrate.py), in
+the format of src/sglang_decode/planning/policy.py:7-28: ``{"status": "validated",
+"evidence": [...], "rules": [{min_tasks, max_tasks, min_ratio, max_ratio, mode}]}``.
+Without a policy the plan runs R1.  A file must say it was validated and carry its
+evidence; rules may select R1, STATIC, D1 or D4 over task-count and weight-ratio ranges
+(the device plan lets the last matching rule win).
 """
 import json
 from dataclasses import dataclass
@@ -19,17 +21,28 @@ class PolicyRule:
     mode: int
 
 
+_SELECTABLE = (Mode.R1, Mode.STATIC, Mode.D1, Mode.D4)
+
+
 def load_policy(path=None):
+    """The rules of a validated policy file, or [] without one (ValueError otherwise)."""
     if path is None:
         return []
     with open(path, encoding="utf-8") as f:
-        data = json.load(f)
-    if data.get("status") != "validated" or not data.get("evidence"):
-        raise ValueError("only explicitly validated policy artifacts may select a dynamic path")
-    rules = [PolicyRule(**row) for row in data["rules"]]
-    for rule in rules:
-        if rule.mode not in (Mode.R1, Mode.STATIC, Mode.D1, Mode.D4):
-            raise ValueError("invalid policy mode")
-        if rule.min_tasks < 0 or rule.max_tasks < rule.min_tasks or rule.min_ratio < 100:
-            raise ValueError("invalid policy bounds")
+        artifact = json.load(f)
+    if artifact.get("status") != "validated":
+        raise ValueError(f"load_policy: {path} is not marked validated; only a calibrated artifact may "
+                         "switch schedules")
+    if not artifact.get("evidence"):
+        raise ValueError(f"load_policy: {path} carries no calibration evidence")
+    rules = []
+    for i, row in enumerate(artifact["rules"]):
+        rule = PolicyRule(**row)
+        if rule.mode not in _SELECTABLE:
+            raise ValueError(f"load_policy: rule {i} selects mode {rule.mode}; a rule may select R1, STATIC, "
+                             "D1 or D4")
+        if not 0 <= rule.min_tasks <= rule.max_tasks or rule.min_ratio < 100:
+            raise ValueError(f"load_policy: rule {i} has empty or negative task bounds, or a weight ratio "
+                             "below 100 (max/min x 100 is at least 100)")
+        rules.append(rule)
     return rules

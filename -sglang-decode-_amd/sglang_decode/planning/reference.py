@@ -1,24 +1,29 @@
-"""Host-side planning: the CPU planning API and the strong host static baseline.
+"""Host-side planning API (the CPU planning spec of src/sglang_decode/planning/reference.py:6-76).
 
-Same functions and results as src/sglang_decode/planning/reference.py:6-76:
+The names, arguments and results are the reference's; the computation is this
+module's own: each stage is one pass over numpy arrays of the batch, and the LPT
+lists come from the native library's C++ heap planner.
 
-* ``split_records`` -- chunk = ceil(ceil(L/S)/32)*32, count = ceil(L/chunk), one
-  record (request, split, begin, end, weight=ceil((end-begin)/block_kv)) per split,
-  raising ValueError on capacity violations (reference.py:15-30);
-* ``bucket_order`` -- records stably ordered heaviest ceil-log2 bucket first
-  (reference.py:33-34);
-* ``make_packs`` -- per bucket, reserve one worker wave of singleton tasks and
-  pack the rest ``width = min(limit, max(1, max_w >> bucket))`` wide
-  (reference.py:37-54);
-* ``greedy_static`` -- longest-processing-time lists with (load, worker) tie
-  breaks (reference.py:57-67).  ``host_static_lists`` returns the same lists as
-  the device's ``static_head``/``static_next`` arrays, computed by the native
-  library's C++ heap planner (used for the host-static variant that uploads its
-  lists, benchmarks/bench_decode.py:14-30);
-* ``validate_plan`` -- coverage and slot uniqueness (reference.py:70-76).
+* ``split_records(lengths, splits, config)`` -> (records, counts, offsets).  A request
+  of L tokens asking for S splits is cut into chunks of c = ceil(ceil(L/S)/32)*32
+  tokens, n = ceil(L/c) of them (0 when L is 0); record i of the request covers
+  [i*c, min((i+1)*c, L)) and weighs ceil(tokens/block_kv).  Records are numbered
+  request-major.  Shapes or values outside the configuration raise ValueError.
+* ``bucket_order(records)`` -> record ids ordered by decreasing bucket, bucket(w) =
+  bit length of w-1 (= ceil(log2 w)), ties kept in id order.
+* ``make_packs(records, order, groups, workers, pack_limit=4)`` -> [(first task,
+  tasks)]: per bucket of the order, its tasks (records x groups, consecutive) are cut
+  into packs of width min(pack_limit, max(1, max_weight >> bucket)) except for the
+  last `workers` tasks (rounded so that the packs are whole), which stay single.
+* ``greedy_static(records, groups, workers)`` -> per-worker task lists: tasks by
+  decreasing weight then id, each given to the worker with the least (load, id).
+* ``lists_to_links`` / ``validate_plan``: the lists as static_head/static_next arrays,
+  and the plan invariants (order a permutation, packs covering every task once, no two
+  tasks on one (request, split, head) slot).
 """
 from dataclasses import dataclass
-import heapq
+
+import numpy as np
 
 
 @dataclass(frozen=True)
@@ -30,84 +35,122 @@ class Record:
     weight: int
 
 
+def _ceil_div(a, b):
+    return -(-a // b)
+
+
+def _record_arrays(lengths, splits, config):
+    """Columns (request, split, begin, end, weight) of the batch's records plus the
+    per-request counts and offsets, as int64 numpy arrays."""
+    length = np.asarray(lengths, dtype=np.int64).reshape(-1)
+    want = np.asarray(splits, dtype=np.int64).reshape(-1)
+    if length.shape != want.shape:
+        raise ValueError(f"split_records: {length.size} lengths but {want.size} split counts")
+    if length.size > config.batch_capacity:
+        raise ValueError(f"split_records: batch {length.size} exceeds batch_capacity {config.batch_capacity}")
+    bad = (length < 0) | (length > config.max_context) | (want < 1) | (want > config.max_splits)
+    if bad.any():
+        r = int(np.flatnonzero(bad)[0])
+        raise ValueError(f"split_records: request {r} has length {int(length[r])} (allowed 0..{config.max_context}) "
+                         f"and {int(want[r])} splits (allowed 1..{config.max_splits})")
+    chunk = _ceil_div(_ceil_div(length, want), 32) * 32
+    count = np.where(chunk > 0, _ceil_div(length, np.maximum(chunk, 1)), 0)
+    offsets = np.concatenate(([0], np.cumsum(count)))
+    request = np.repeat(np.arange(length.size), count)
+    split = np.arange(int(offsets[-1])) - offsets[request]
+    begin = split * chunk[request]
+    end = np.minimum(begin + chunk[request], length[request])
+    weight = _ceil_div(end - begin, config.block_kv)
+    return (request, split, begin, end, weight), count, offsets
+
+
 def split_records(lengths, requested_splits, config):
-    if len(lengths) != len(requested_splits) or len(lengths) > config.batch_capacity:
-        raise ValueError("batch/split shape exceeds the capture contract")
-    records, offsets, counts = [], [0], []
-    for request, (length, splits) in enumerate(zip(lengths, requested_splits)):
-        if not 0 <= length <= config.max_context or not 1 <= splits <= config.max_splits:
-            raise ValueError("invalid length or split count")
-        chunk = -(-(-(-length // splits)) // 32) * 32
-        count = -(-length // chunk) if chunk else 0
-        counts.append(count)
-        for split in range(count):
-            begin = split * chunk
-            end = min(begin + chunk, length)
-            records.append(Record(request, split, begin, end,
-                                  -(-(end - begin) // config.block_kv)))
-        offsets.append(len(records))
-    return records, counts, offsets
+    cols, count, offsets = _record_arrays(lengths, requested_splits, config)
+    records = [Record(*row) for row in zip(*(c.tolist() for c in cols))]
+    return records, count.tolist(), offsets.tolist()
 
 
-def _bucket(weight):
-    return (weight - 1).bit_length()
+def _weights(records):
+    return np.fromiter((r.weight for r in records), dtype=np.int64, count=len(records))
+
+
+def _buckets(weight):
+    """Bit length of w - 1 for every weight (0 for w <= 1)."""
+    v = np.maximum(np.asarray(weight, dtype=np.int64) - 1, 0)
+    bits = np.zeros_like(v)
+    while v.any():
+        bits += v > 0
+        v >>= 1
+    return bits
 
 
 def bucket_order(records):
-    return sorted(range(len(records)), key=lambda i: -_bucket(records[i].weight))
+    return np.argsort(-_buckets(_weights(records)), kind="stable").tolist()
 
 
 def make_packs(records, order, groups, workers, pack_limit=4):
-    """Pack within one bucket; reserve a full worker wave of singleton tasks."""
-    packs = []
-    max_weight = max((r.weight for r in records), default=1)
-    first = 0
-    while first < len(order):
-        bucket = _bucket(records[order[first]].weight)
-        last = first
-        while last < len(order) and _bucket(records[order[last]].weight) == bucket:
-            last += 1
-        tasks = (last - first) * groups
-        width = min(pack_limit, max(1, max_weight >> bucket))
-        packed = max(0, tasks - workers) // width * width
-        base = first * groups
-        packs.extend((base + i, width) for i in range(0, packed, width))
-        packs.extend((base + i, 1) for i in range(packed, tasks))
-        first = last
-    return packs
+    if not records:
+        return []
+    weight = _weights(records)
+    bucket = _buckets(weight)[np.asarray(order, dtype=np.int64)]
+    top = int(weight.max())
+    # runs of equal bucket along the order: [start, stop) in records
+    cuts = np.flatnonzero(np.diff(bucket)) + 1
+    starts = np.concatenate(([0], cuts))
+    stops = np.concatenate((cuts, [bucket.size]))
+    firsts, widths = [], []
+    for start, stop, b in zip(starts.tolist(), stops.tolist(), bucket[starts].tolist()):
+        tasks = (stop - start) * groups
+        width = min(pack_limit, max(1, top >> b))
+        wide = max(0, tasks - workers) // width * width
+        base = start * groups
+        firsts.append(base + np.arange(0, wide, width))
+        widths.append(np.full(wide // width, width))
+        firsts.append(base + np.arange(wide, tasks))
+        widths.append(np.ones(tasks - wide, dtype=np.int64))
+    first, width = np.concatenate(firsts), np.concatenate(widths)
+    return list(zip(first.tolist(), width.tolist()))
 
 
 def greedy_static(records, groups, workers):
-    """LPT lists: tasks by (-weight, task id), each to the least (load, worker)."""
-    tasks = sorted(range(len(records) * groups), key=lambda t: (-records[t // groups].weight, t))
-    heap = [(0, w) for w in range(workers)]
-    lists = [[] for _ in range(workers)]
-    for task in tasks:
-        load, worker = heapq.heappop(heap)
-        lists[worker].append(task)
-        heapq.heappush(heap, (load + records[task // groups].weight, worker))
+    from .host_static import host_static_lists
+    tasks = len(records) * groups
+    heads, nxt = host_static_lists(_weights(records), groups, workers, max(tasks, 1))
+    lists = []
+    for head in heads.tolist():
+        chain, t = [], head
+        while t >= 0:
+            chain.append(t)
+            t = int(nxt[t])
+        lists.append(chain)
     return lists
 
 
 def lists_to_links(lists, workers, task_capacity):
     """Per-worker lists -> (static_head[workers], static_next[task_capacity]), -1 terminated."""
-    heads = [-1] * workers
-    links = [-1] * task_capacity
-    for worker, tasks in enumerate(lists):
-        if tasks:
-            heads[worker] = tasks[0]
-        for left, right in zip(tasks, tasks[1:]):
-            links[left] = right
-    return heads, links
+    heads = np.full(workers, -1, dtype=np.int64)
+    links = np.full(task_capacity, -1, dtype=np.int64)
+    for worker, chain in enumerate(lists):
+        if chain:
+            heads[worker] = chain[0]
+            links[np.asarray(chain[:-1], dtype=np.int64)] = chain[1:]
+    return heads.tolist(), links.tolist()
 
 
 def validate_plan(records, order, packs, groups):
-    if sorted(order) != list(range(len(records))):
-        raise AssertionError("order is not a permutation of the records")
-    tasks = [task for first, count in packs for task in range(first, first + count)]
-    if sorted(tasks) != list(range(len(records) * groups)):
-        raise AssertionError("packs do not cover every task exactly once")
-    slots = {(records[order[t // groups]].request, records[order[t // groups]].split,
-              t % groups) for t in tasks}
-    if len(slots) != len(tasks):
-        raise AssertionError("two tasks write the same (request, split, head) slot")
+    n = len(records)
+    if sorted(order) != list(range(n)):
+        raise AssertionError("validate_plan: the order must list every record exactly once")
+    covered = np.zeros(n * groups, dtype=np.int64)
+    for first, count in packs:
+        covered[first:first + count] += 1
+    if covered.size and (covered != 1).any():
+        raise AssertionError(f"validate_plan: task {int(np.flatnonzero(covered != 1)[0])} is scheduled "
+                             f"{int(covered[covered != 1][0])} times")
+    if sum(count for _, count in packs) != n * groups:
+        raise AssertionError("validate_plan: the packs schedule more tasks than exist")
+    ordered = np.asarray(order, dtype=np.int64)
+    key = {(records[ordered[t // groups]].request, records[ordered[t // groups]].split, t % groups)
+           for t in range(n * groups)}
+    if len(key) != n * groups:
+        raise AssertionError("validate_plan: two tasks write one (request, split, head) slot")

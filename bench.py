@@ -278,16 +278,14 @@ def main():
         fx = [W.make_csr_inputs(c, lengths, seed=1000 + i, device=dev, pool_tokens=pool_tokens, dtype=dtype,
                                 device_pool=True) for i in range(pools)]
         fx = [fx[i % pools] for i in range(layers)]
-        graph_kw = dict(indptrs=[x[4].numel() for x in fx])
+        graph_kw = dict(index_capacity=[x[4].numel() for x in fx])
         tables = [x[4] for x in fx]
-        update_kw = dict(indptrs=[x[3] for x in fx])
     else:
         fx = [W.make_inputs(c, lengths, seed=1000 + i, device=dev, dtype=dtype, pool_pages=200_000,
                             device_pool=True) for i in range(pools)]
         fx = [fx[i % pools] for i in range(layers)]
         graph_kw = {}
         tables = [x[3][:batch] for x in fx]
-        update_kw = {}
     bytes_per_layer = W.algorithmic_bytes(lengths, c)
     torch.cuda.synchronize()
 
@@ -337,7 +335,7 @@ def main():
             engine.prepare = prepare
         key = PlanKey(args.workload, "hints", (c.query_heads, c.kv_heads, c.head_dim))
         graph = DecodeGraph(engine, [key] * layers, [(x[1], x[2]) for x in fx], **graph_kw)
-        graph.update([x[0][:batch] for x in fx], tables, lengths, splits, **update_kw)
+        graph.update([x[0][:batch] for x in fx], tables, lengths, splits)
         graph.capture()
         for _ in range(args.warmup):
             graph.replay()

@@ -70,7 +70,7 @@ def test_csr_graph_replay_shrinking_batches(mode):
     engine = DecodeEngine(c, layers=layers, force_mode=mode)
     key = PlanKey("batch", "hints", (32, 8, 128))
     graph = DecodeGraph(engine, [key] * layers, [(x[1], x[2]) for x in fx],
-                        indptrs=[x[4].numel() for x in fx])
+                        index_capacity=[x[4].numel() for x in fx])
     for step, batch in enumerate([64, 48, 17, 1]):
         lengths = [x + step for x in base[:batch]]
         # each layer's kv_indices for this step: the first L tokens of each request's slots
@@ -83,7 +83,7 @@ def test_csr_graph_replay_shrinking_batches(mode):
             ptr[1:] = torch.cumsum(torch.tensor(lengths), 0)
             indptrs.append(ptr.cuda())
             indices.append(torch.cat(parts).cuda())
-        graph.update([x[0][:batch] for x in fx], indices, lengths, W.split_hints(lengths, 16), indptrs)
+        graph.update([x[0][:batch] for x in fx], indices, lengths, W.split_hints(lengths, 16))
         if step == 0:
             graph.capture()
         for layer in engine.layers:
@@ -136,13 +136,12 @@ def test_llama8b_32_layer_graph_shrinking_batches():
     engine = DecodeEngine(c, layers=layers, rules=rules)
     key = PlanKey("c5", "hints", (c.query_heads, c.kv_heads, c.head_dim))
     graph = DecodeGraph(engine, [key] * layers, [(x[1], x[2]) for x in fx],
-                        indptrs=[x[4].numel() for x in fx])
+                        index_capacity=[x[4].numel() for x in fx])
     checked = (0, 17, 31)
     for step, batch in enumerate(W.C5_BATCHES):
         lengths = [x + step for x in base[:batch]]
         indptrs, indices = _csr_step(fx, lengths)
-        graph.update([x[0][:batch] for x in fx], indices, lengths, W.split_hints(lengths, c.max_splits),
-                     indptrs)
+        graph.update([x[0][:batch] for x in fx], indices, lengths, W.split_hints(lengths, c.max_splits))
         if step == 0:
             graph.capture()
         for layer in engine.layers:
@@ -154,5 +153,4 @@ def test_llama8b_32_layer_graph_shrinking_batches():
             close(outs[i][:batch], _oracle_layer(fx[i], indptrs[i], indices[i], lengths)[:batch])
     # over capacity: the host refuses before the graph is touched
     with pytest.raises(ValueError):
-        graph.update([x[0][:1] for x in fx], [x[4][:1] for x in fx], [c.max_context + 1], [1],
-                     [torch.tensor([0, 1], dtype=torch.int32, device="cuda")] * layers)
+        graph.update([x[0][:1] for x in fx], [x[4][:1] for x in fx], [c.max_context + 1], [1])

@@ -296,3 +296,39 @@ def test_noalloc_rejects_geometry_beyond_its_scratch_before_any_device_call():
     a.out = None
     assert lib.sgd_decode_noalloc(ctypes.byref(a), None) == -22
     assert b"null buffer" in lib.sgd_last_error()
+
+
+def test_graph_update_checks_on_the_host():
+    """DecodeGraph refuses a step that does not fit before touching any buffer: batch,
+    context and split bounds, per-layer shapes, and in CSR mode kv_indices that hold
+    fewer entries than the lengths need or more than the graph's capacity (the graph
+    derives kv_indptr from the lengths itself, so the two cannot disagree)."""
+    import torch
+    from sglang_decode.runtime.engine import DecodeEngine, PlanKey
+    from sglang_decode.runtime.graph import DecodeGraph
+    c = DecodeConfig(batch_capacity=4, max_splits=4, max_context=256, page_size=1, workers=8)
+    engine = DecodeEngine(c, device="cpu", layers=2)
+    key = PlanKey("x", "hints", (32, 8, 128))
+    kv = (torch.zeros(64, 8, 128, dtype=torch.bfloat16),) * 2
+    with pytest.raises(ValueError, match="same plan key"):
+        DecodeGraph(engine, [key, PlanKey("y", "hints", (32, 8, 128))], [kv] * 2, index_capacity=[64, 64])
+    with pytest.raises(ValueError, match="capacities"):
+        DecodeGraph(engine, [key] * 2, [kv] * 2, index_capacity=[64])
+    graph = DecodeGraph(engine, [key] * 2, [kv] * 2, index_capacity=[64, 32])
+    q = torch.zeros(2, 32, 128, dtype=torch.bfloat16)
+    idx = torch.zeros(40, dtype=torch.int32)
+    with pytest.raises(ValueError, match="batch 5"):
+        graph.update([q] * 2, [idx] * 2, [1] * 5, [1] * 5)
+    with pytest.raises(ValueError, match="context length"):
+        graph.update([q] * 2, [idx] * 2, [10, 300], [1, 1])
+    with pytest.raises(ValueError, match="split count"):
+        graph.update([q] * 2, [idx] * 2, [10, 30], [1, 5])
+    with pytest.raises(ValueError, match="layer 1 kv_indices has 40 entries; the step needs 40 and the graph "
+                                         "holds 32"):
+        graph.update([q] * 2, [idx] * 2, [10, 30], [1, 1])
+    with pytest.raises(ValueError, match="step needs 50"):
+        graph.update([q] * 2, [idx] * 2, [20, 30], [1, 1])
+    with pytest.raises(ValueError, match="layer 0 q"):
+        graph.update([q[:1]] * 2, [idx] * 2, [10, 30], [1, 1])
+    with pytest.raises(RuntimeError, match="update"):
+        graph.capture()
