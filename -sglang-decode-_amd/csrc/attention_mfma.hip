@@ -50,8 +50,13 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// A head's row of a wave's output is padded by 4 floats: in the 16-byte stores of the
+// end-of-task merge the 16 heads of a lane group then start 4 banks apart instead of
+// all on the same bank (a 128-float stride is a multiple of the bank count).
+constexpr int kOPad = 4;
+
 struct MfmaShared {
-    float o[kWaves][kHeadsM][kD];  // per-wave unnormalized outputs, 32 KB
+    float o[kWaves][kHeadsM][kD + kOPad];  // per-wave unnormalized outputs, 33 KB
     float m[kWaves][kHeadsM];
     float d[kWaves][kHeadsM];
     int32_t cursor;

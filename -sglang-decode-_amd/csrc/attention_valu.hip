@@ -9,7 +9,8 @@
 //
 // Worker = one workgroup of kWaves waves (8: two workgroups per CU, or 16: one),
 // 16 waves per CU in both cases -- the load concurrency the random 256 B row
-// gathers need.  Tasks come from the plan's dispatch (attention_common.h); each
+// gathers need, and enough waves to hide the tile math (~395 VALU instructions per
+// tile and wave, about 40% of the SIMDs' issue slots over a launch).  Tasks come from the plan's dispatch (attention_common.h); each
 // task (record, kv head) is dealt to the waves in 16-token tiles (tile i -> wave
 // i % kWaves).  Per wave and tile: gather K and V rows (4 x 16 B loads each), stage
 // them in the wave's LDS tile shared by the group's query heads, QK^T with a DPP
