@@ -393,88 +393,131 @@ __device__ void stage_order_and_packs(const int32_t *weight, int32_t total, int3
 }
 
 // ---------------------------------------------------------------- STATIC lists
-// Longest-processing-time assignment: records in (-weight, record) order, each
-// record's kv_heads tasks in task order, each task to the worker with the least
-// (load, worker).  Records are sorted once (bitonic, in LDS); the assignment loop
-// runs on wave 0 with every lane caching the minimum of its share of workers.
+// Longest-processing-time assignment (kernels/plan.py:103-135, planning/reference.py:
+// 57-67): tasks in (-weight, task) order, each to the worker with the least (load,
+// worker).  The records are sorted once (bitonic, in LDS); the assignment runs in
+// rounds that are provably the sequential choice:
+//
+// Keep the workers sorted by key (load << 32 | worker).  Within a run of tasks of equal
+// weight w, with S the sorted keys and T = S[0] + (w << 32) (the first worker's key
+// after it takes a task), let k = #{i : S[i] < T}.  Sequentially, the next k tasks go
+// to S[0], S[1], ..., S[k-1] in that order: when S[i] (i < k) is due, every worker
+// already given a task this round has key S[j] + (w << 32) >= T > S[i] (S[j] <= S[i]),
+// and every other worker has a key >= S[i]; after S[k-1] the least key is T, S[0]'s.
+// So a round assigns min(k, tasks left in the run) tasks at once, then merges the
+// raised keys S[0..m) + (w << 32) (still sorted) with the untouched S[m..) (sorted)
+// by binary-search placement.  Keys are distinct (distinct workers), so the merge has
+// no ties.  A balanced plan takes about tasks / workers rounds; any plan at most one
+// round per task.  Each list is written as it grows: a worker's first task to
+// static_head, each later one to static_next of its previous task, and a final pass
+// terminates the lists (every entry is written once, so no ordering between the
+// rounds' global stores is needed).
 constexpr int kGreedyMaxRecords = 16384;
 constexpr int kGreedyMaxWorkers = 4096;
 
-struct GreedyShared {
-    uint32_t keys[kGreedyMaxRecords];     // (0xffff - weight) << 16 | record, sorted ascending
-    int32_t load[kGreedyMaxWorkers];
-    int32_t tail[kGreedyMaxWorkers];
+struct LptLds {
+    uint64_t key[2][kGreedyMaxWorkers];  // sorted worker keys, double-buffered across rounds
+    int32_t tail[kGreedyMaxWorkers];     // each worker's last task, -1 before its first
 };
 
-// keys / load / tail are LDS arrays of kGreedyMaxRecords / workers entries.  weight may
-// alias keys (the fused kernel's LDS weights become the keys in place: each index is
-// read and then written by the same thread).
-__device__ void stage_greedy_lists(const int32_t *weight, int32_t total, int32_t mode,
-                                   int32_t *static_head, int32_t *static_next, int32_t hkv,
-                                   int32_t workers, uint32_t *keys, int32_t *load, int32_t *tail) {
-    struct {
-        uint32_t *keys;
-        int32_t *load, *tail;
-    } g{keys, load, tail};
+struct GreedyShared {
+    uint32_t keys[kGreedyMaxRecords];  // (0xffff - weight) << 16 | record, sorted ascending
+    LptLds lpt;
+};
+
+// First index i in [lo, hi) with a[i] >= x (a ascending), by binary search.
+__device__ __forceinline__ int32_t lower_bound_u64(const uint64_t *a, int32_t lo, int32_t hi, uint64_t x) {
+    while (lo < hi) {
+        const int32_t mid = (lo + hi) >> 1;
+        if (a[mid] < x) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// keys: LDS array of kGreedyMaxRecords entries; weight may alias it (the fused kernel's
+// LDS weights become the keys in place: each index is read and then written by the same
+// thread).
+__device__ void stage_greedy_lists(const int32_t *weight, int32_t total, int32_t mode, int32_t *static_head,
+                                   int32_t *static_next, int32_t hkv, int32_t workers, uint32_t *keys,
+                                   LptLds &g) {
     if (mode != 2) return;
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x;
     int n2 = 1;
     while (n2 < total) n2 <<= 1;
     for (int i = tid; i < n2; i += kPlanThreads)
-        g.keys[i] = i < total ? ((uint32_t)(0xffff - weight[i]) << 16) | (uint32_t)i : 0xffffffffu;
+        keys[i] = i < total ? ((uint32_t)(0xffff - weight[i]) << 16) | (uint32_t)i : 0xffffffffu;
     for (int w = tid; w < workers; w += kPlanThreads) {
-        g.load[w] = 0;
+        g.key[0][w] = (uint64_t)(uint32_t)w;  // load 0: sorted by worker
         g.tail[w] = -1;
-        static_head[w] = -1;
     }
-    __syncthreads();  // also orders the static_head stores before wave 0 rewrites them
+    lds_barrier();
     for (int k = 2; k <= n2; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
             for (int i = tid; i < n2; i += kPlanThreads) {
                 const int p = i ^ j;
                 if (p > i) {
-                    const uint32_t a = g.keys[i], b = g.keys[p];
+                    const uint32_t a = keys[i], b = keys[p];
                     const bool up = (i & k) == 0;
-                    if ((a > b) == up) { g.keys[i] = b; g.keys[p] = a; }
+                    if ((a > b) == up) { keys[i] = b; keys[p] = a; }
                 }
             }
             lds_barrier();
         }
     }
-    if (tid >= 64) return;
-    // lane l owns workers l, l+64, ...; cache (load << 32 | worker) of its minimum.
-    auto local_min = [&]() {
-        uint64_t best = ~0ull;
-        for (int w = lane; w < workers; w += 64) {
-            const uint64_t key = ((uint64_t)(uint32_t)g.load[w] << 32) | (uint32_t)w;
-            best = key < best ? key : best;
+    const int64_t ntasks = (int64_t)total * hkv;
+    int cur = 0;
+    for (int64_t q = 0; q < ntasks;) {
+        // the run of records with the weight of sorted record q / hkv
+        const uint32_t hi = keys[q / hkv] >> 16;
+        const int32_t w = 0xffff - (int32_t)hi;
+        int32_t lo_r = (int32_t)(q / hkv) + 1, hi_r = total;  // first sorted record of another weight
+        while (lo_r < hi_r) {
+            const int32_t mid = (lo_r + hi_r) >> 1;
+            if ((keys[mid] >> 16) == hi) lo_r = mid + 1;
+            else hi_r = mid;
         }
-        return best;
-    };
-    uint64_t mine = local_min();
-    for (int r = 0; r < total; ++r) {
-        const uint32_t key = g.keys[r];
-        const int32_t rec = (int32_t)(key & 0xffff);
-        const int32_t w = 0xffff - (int32_t)(key >> 16);
-        for (int h = 0; h < hkv; ++h) {
-            uint64_t best = mine;
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const uint64_t other = __shfl_xor(best, o, 64);
-                best = other < best ? other : best;
+        const int64_t run_end = (int64_t)lo_r * hkv;
+        while (q < run_end) {
+            const uint64_t *S = g.key[cur];
+            uint64_t *out = g.key[cur ^ 1];
+            const uint64_t raise = (uint64_t)(uint32_t)w << 32;
+            const int32_t k = lower_bound_u64(S, 1, workers, S[0] + raise);
+            const int32_t m = (int32_t)min((int64_t)k, run_end - q);
+            for (int i = tid; i < workers; i += kPlanThreads) {
+                const uint64_t s = S[i];
+                if (i < m) {
+                    // task q + i of the sorted stream goes to worker S[i]
+                    const int64_t qi = q + i;
+                    const int32_t rec = (int32_t)(keys[qi / hkv] & 0xffff);
+                    const int32_t task = rec * hkv + (int32_t)(qi % hkv);
+                    const int32_t worker = (int32_t)(uint32_t)s;
+                    const int32_t prev = g.tail[worker];
+                    if (prev < 0) static_head[worker] = task;
+                    else static_next[prev] = task;
+                    g.tail[worker] = task;
+                    const uint64_t up = s + raise;
+                    out[i + lower_bound_u64(S, m, workers, up) - m] = up;
+                } else {
+                    // untouched key: behind the raised keys below it
+                    int32_t lo = 0, hi2 = m;
+                    while (lo < hi2) {
+                        const int32_t mid = (lo + hi2) >> 1;
+                        if (S[mid] + raise < s) lo = mid + 1;
+                        else hi2 = mid;
+                    }
+                    out[(i - m) + lo] = s;
+                }
             }
-            const int owner = (int)(best & 0xffffffffu);
-            const int32_t task = rec * hkv + h;
-            if (lane == (owner & 63)) {
-                const int32_t t = g.tail[owner];
-                if (t < 0) static_head[owner] = task;
-                else static_next[t] = task;
-                static_next[task] = -1;
-                g.tail[owner] = task;
-                g.load[owner] += w;
-                mine = local_min();
-            }
+            lds_barrier();
+            cur ^= 1;
+            q += m;
         }
+    }
+    for (int w = tid; w < workers; w += kPlanThreads) {
+        const int32_t last = g.tail[w];
+        if (last < 0) static_head[w] = -1;
+        else static_next[last] = -1;
     }
 }
 
@@ -548,25 +591,24 @@ __global__ __launch_bounds__(kPlanThreads) void k_greedy_lists(const int32_t *we
                                                                int32_t workers) {
     extern __shared__ char dyn[];
     GreedyShared &g = *reinterpret_cast<GreedyShared *>(dyn);
-    stage_greedy_lists(weight, *record_count, *mode, static_head, static_next, hkv, workers, g.keys, g.load,
-                       g.tail);
+    stage_greedy_lists(weight, *record_count, *mode, static_head, static_next, hkv, workers, g.keys, g.lpt);
 }
 
 // Dynamic LDS of the fused kernel.  Region A holds the per-row values (lengths,
-// offsets, chunks) from count/scan through the dispatch table, then the LPT
-// loads/tails; the order mirror (int16: records < 16384) serves the dispatch table;
-// region B holds the record weights between emission, ordering and the LPT, where they
-// become the sort keys.
+// offsets, chunks) from count/scan through the dispatch table, with the order mirror
+// (int16: records < 16384) that the dispatch table reads; the LPT's worker keys and
+// tails take it over afterwards.  Region B holds the record weights between emission,
+// ordering and the LPT, where they become the sort keys.
 struct FusedLds {
     union {
         struct {
-            int32_t lengths[4096], offsets[4097], chunk[4096];
-        } rows;
-        struct {
-            int32_t load[kGreedyMaxWorkers], tail[kGreedyMaxWorkers];
-        } lpt;
+            struct {
+                int32_t lengths[4096], offsets[4097], chunk[4096];
+            } rows;
+            int16_t order[kGreedyMaxRecords];
+        } pre;
+        LptLds lpt;
     } a;
-    int16_t order[kGreedyMaxRecords];
     union {
         int32_t weight[kGreedyMaxRecords];
         uint32_t keys[kGreedyMaxRecords];
@@ -590,7 +632,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p,
     static_assert(5 * kLdsRules <= kPlanThreads, "one rule int per thread");
     const bool rules_lds = p.rule_count <= kLdsRules;
     const int32_t rule_v = p.rules[min((int)threadIdx.x, 5 * max(p.rule_count, 1) - 1)];
-    const RowMirror mirror{L.a.rows.lengths, nullptr, L.a.rows.offsets, L.a.rows.chunk};
+    const RowMirror mirror{L.a.pre.rows.lengths, nullptr, L.a.pre.rows.offsets, L.a.pre.rows.chunk};
     const CsrRows csr{csr_indptr, csr_splits, csr_batch, p.lengths, p.splits, p.active};
     stage_count_scan(p.lengths, p.splits, p.active, p.counts, p.offsets, p.chunk, p.record_count, p.error,
                      p.batch_capacity, p.max_splits, p.max_context, sh, &mirror, csr_indptr ? &csr : nullptr);
@@ -607,17 +649,17 @@ __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p,
     stage_order_and_packs(L.b.weight, total, p.order, p.pack_first, p.pack_count, p.num_packs, p.mode,
                           rules_lds ? sh.rules : p.rules,
                           p.rule_count, force, p.kv_heads, p.workers, p.buckets, p.batch_capacity * p.max_splits,
-                          sh, L.order);
+                          sh, L.a.pre.order);
     if (p.dispatch) {
         lds_barrier();
-        stage_dispatch_table(p.dispatch, p.batch_capacity * p.max_splits * p.kv_heads, L.order, mirror,
+        stage_dispatch_table(p.dispatch, p.batch_capacity * p.max_splits * p.kv_heads, L.a.pre.order, mirror,
                              p.batch_capacity, total, p.kv_heads, p.buckets, sh);
     }
     if (run_greedy) {
         lds_barrier();
-        // the LPT's loads and tails take region A (free by now), its keys replace the weights
+        // the LPT's worker keys and tails take region A (free by now), its keys replace the weights
         stage_greedy_lists(L.b.weight, total, sh.mode, p.static_head, p.static_next, p.kv_heads, p.workers,
-                           L.b.keys, L.a.lpt.load, L.a.lpt.tail);
+                           L.b.keys, L.a.lpt);
     }
 }
 

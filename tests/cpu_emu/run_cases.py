@@ -2,7 +2,8 @@
 infrastructure).  Meant to run in its own process with the ASan build; ``spawn()``
 starts it with clang's ASan runtime preloaded.
 
-A case is a JSON object: {"sweep": seed} (the GPU sweep's draw of that seed, every
+A case is a JSON object: {"lpt": trials} (random STATIC-list plans against the oracle's
+sequential LPT, one JSON line with the mismatch count), {"sweep": seed} (the GPU sweep's draw of that seed, every
 kernel that takes its shape), or {"workload": "c1".."c5", "modes": [...], "kernels":
 [...], "requests": n} (a named configuration, optionally its first n requests).  One
 JSON line per (case, kernel, mode) goes to stdout: violations of the 2e-2 abs / 1e-2 rel
@@ -68,11 +69,50 @@ def _check(emu, c, lengths, splits, inputs, expected, mode, kernel, scale, dtype
         npk = ref["num_packs"]
         plan_ok = plan_ok and p["pack_first"][:npk] == ref["pack_first"] and p["pack_count"][:npk] == ref[
             "pack_count"]
+    if plan_ok and "static_head" in ref:  # STATIC: the per-worker lists, walked
+        plan_ok = OP.walk_lists(p["static_head"], p["static_next"]) == OP.walk_lists(ref["static_head"],
+                                                                                     ref["static_next"])
     return dict(case=tag, kernel=r["kernel"], mode=int(mode), dtype=dtype_name,
                 violations=int((np.abs(o - e) > 2e-2 + 1e-2 * np.abs(e)).sum()),
                 nans=int(np.isnan(o).sum()), tail=float(np.abs(r["out"][n:]).sum()),
                 plan_ok=bool(plan_ok), counters=r["sync"], max_err=float(np.nan_to_num(np.abs(o - e), nan=9.0).max())
                 if o.size else 0.0)
+
+
+def _lpt_trials(emu, trials, seed):
+    """The device STATIC lists (sgd_greedy_lists: round-based LPT) against the oracle's
+    sequential argmin LPT on random weights: batches of 0-300 records, 1-8 kv heads,
+    1-512 workers; weights uniform in 1..4, in 1..128, mostly 1 with 5% of them 64..200
+    (loads far apart, so rounds of a few tasks), or all equal.  Returns the number of
+    trials whose walked lists differ."""
+    import numpy as np
+    import driver as D
+    from oracle import plan as OP
+    rng = np.random.default_rng(seed)
+    bad = []
+    for trial in range(trials):
+        n = int(rng.integers(0, 300))
+        workers = int(rng.choice([1, 2, 3, 7, 16, 40, 108, 256, 512]))
+        hkv = int(rng.choice([1, 2, 8]))
+        kind = trial % 4
+        if kind == 0:
+            w = rng.integers(1, 5, n)
+        elif kind == 1:
+            w = rng.integers(1, 129, n)
+        elif kind == 2:
+            w = np.where(rng.random(n) < 0.05, rng.integers(64, 200, n), 1)
+        else:
+            w = np.full(n, int(rng.integers(1, 9)))
+        cap = max(n, 1)
+        wd = emu.upload(np.asarray(w, np.int32) if n else np.zeros(1, np.int32))
+        count, mode = emu.upload(np.array([n], np.int32)), emu.upload(np.array([2], np.int32))
+        head, nxt = emu.array((workers,), np.int32, 77), emu.array((cap * hkv,), np.int32, 77)
+        emu.check(emu.lib.sgd_greedy_lists(D.ptr(wd), D.ptr(count), D.ptr(mode), D.ptr(head), D.ptr(nxt), hkv,
+                                           workers, cap, None), "greedy_lists")
+        ref_head, ref_next = OP.greedy_lists([int(x) for x in w], n, 2, hkv, workers, cap * hkv)
+        if OP.walk_lists(head.tolist(), nxt.tolist()) != OP.walk_lists(ref_head, ref_next):
+            bad.append(dict(trial=trial, records=n, workers=workers, kv_heads=hkv, kind=kind))
+    return dict(case="lpt", trials=trials, mismatches=len(bad), first=bad[:3])
 
 
 def run(cases, asan):
@@ -81,7 +121,9 @@ def run(cases, asan):
     sys.path.insert(0, TESTS)
     emu = D.Emu(asan=asan)
     for case in cases:
-        if "sweep" in case:
+        if "lpt" in case:
+            print(json.dumps(_lpt_trials(emu, int(case["lpt"]), int(case.get("seed", 0)))), flush=True)
+        elif "sweep" in case:
             from test_gpu_sweep import draw, kernels_for
             seed = int(case["sweep"])
             c, csr, lengths, splits, dtype, mode, scale = draw(seed)

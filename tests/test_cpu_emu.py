@@ -102,3 +102,15 @@ print("no report")
     assert p.returncode != 0, p.stdout
     assert "heap-buffer-overflow" in p.stderr, p.stderr[-3000:]
     assert "k_merge" in p.stderr, p.stderr[-3000:]
+
+
+def test_static_lists_rounds_match_sequential_lpt(asan_build):
+    """The device STATIC lists are assigned in rounds of equal-weight tasks (csrc/plan.hip
+    stage_greedy_lists); on 80 random plans -- uniform, spread and mostly-light weights
+    with a few heavy records (loads far apart: rounds of a few tasks), 1 to 512 workers --
+    the walked lists equal the oracle's one-task-at-a-time (load, worker) argmin LPT
+    (kernels/plan.py:103-135), in bounds under AddressSanitizer."""
+    rc, rows, err = _run([{"lpt": 80, "seed": 3}])
+    assert rc == 0, err[-4000:]
+    assert "ERROR: AddressSanitizer" not in err, err[-4000:]
+    assert rows and rows[0]["mismatches"] == 0, rows
