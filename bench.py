@@ -93,6 +93,8 @@ def parse():
     ap.add_argument("--plan-inputs", action="store_true",
                     help="also time the plan build reading kv_indptr / num_kv_splits itself against the "
                          "reference adapter's copies before it")
+    ap.add_argument("--no-upstream", action="store_true",
+                    help="skip the upstream two-stage split-KV comparator leg (CSR workloads, groups <= 4)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run a plain N-MiB read+write kernel 5 times, so a rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE pass can scale its counts to bytes")
@@ -474,6 +476,35 @@ def main():
     print(f"[bench] attention + merge ({best}): {attn_merge_us:.2f} us/layer; single-layer full entry "
           f"(plan + attention + merge): {single_layer_us:.2f} us", flush=True)
 
+    # the reference benchmark's external comparator (benchmarks/baselines.py:8-34): upstream
+    # SGLang's two-stage split-KV decode on the same inputs and split counts, per layer over the
+    # same rotating pools, captured in a HIP graph like the attention + merge figure
+    upstream = None
+    if csr and not args.no_upstream and c.group_size <= 4:
+        from sglang_decode.kernels.upstream import decode_attention_fwd
+        num = torch.tensor(splits, dtype=torch.int32, device=dev)
+        up_logits = torch.empty((batch, c.query_heads, c.max_splits, c.head_dim), device=dev)
+        up_lse = torch.empty((batch, c.query_heads, c.max_splits), device=dev)
+        up_out = [torch.empty((batch, c.query_heads, c.head_dim), dtype=dtype, device=dev) for _ in range(pools)]
+
+        def up_call(i):
+            x = fx[i % layers]
+            decode_attention_fwd(x[0][:batch], x[1], x[2], up_out[i % pools], x[3][:batch + 1], x[4], up_logits, up_lse,
+                                 num, c.max_splits, c.head_dim ** -0.5)
+
+        up_us = graph_time(up_call, layers, dev)
+        up_check = None
+        if expected is not None:
+            up_call(0)
+            torch.cuda.synchronize()
+            got = up_out[0].float().cpu().numpy()
+            up_check = dict(ok=bool(np.allclose(got, expected, atol=2e-2, rtol=1e-2)),
+                            max_abs_err=round(float(np.max(np.abs(got - expected))), 6))
+        upstream = dict(us_per_layer=round(up_us, 2), gbps=round(bytes_per_layer / (up_us * 1e-6) / 1e9, 1),
+                        check=up_check, splits=f"split_hints(L, {c.max_splits})")
+        print(f"[bench] upstream two-stage split-KV (gfx950 rebuild): {up_us:.2f} us/layer "
+              f"({upstream['gbps']:.0f} GB/s), check {up_check}", flush=True)
+
     plan_inputs = None
     if args.plan_inputs:
         plan_inputs = time_plan_inputs(c, lengths, splits, dev)
@@ -587,6 +618,7 @@ def main():
         "attention_merge_us": round(attn_merge_us, 2),
         "single_layer_entry_us": round(single_layer_us, 2),
         "entry": entry,
+        "upstream_comparator": upstream,
     }
     if kv_store is not None:
         line["kv_store"] = kv_store

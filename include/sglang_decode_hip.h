@@ -255,6 +255,27 @@ int sgd_host_static_lists(const int32_t *weight, int32_t record_count, int32_t k
                           int32_t workers, int32_t task_capacity, int32_t *static_head,
                           int32_t *static_next);
 
+/*
+ * Upstream SGLang's two-stage split-KV decode on gfx950: the comparator of the reference's
+ * benchmark (benchmarks/baselines.py:8-34, over third_party/sglang/decode_attention.py:
+ * 245-601 of SGLang v0.4.6.post5: decode_attention_fwd with its grouped stage 1 and its
+ * stage 2).  Not on the persistent path.  CSR KV through kv_indptr [batch + 1] /
+ * kv_indices; k/v [tokens, kv_heads, 128] with kv_strides = {k token, k head, v token, v
+ * head} element strides (unit dim stride), q [batch, Hq, 128] with q_strides.  Stage 1: a
+ * grid program per (split s < max_kv_splits, kv head, request b) over tokens [s*c,
+ * min((s+1)*c, L_b)), c = ceil(ceil(L_b / S_b) / 32) * 32, S_b = num_kv_splits[b] (clamped
+ * to [1, max_kv_splits]), writing the normalized partial and natural-log LSE of each q head
+ * to attn_out [batch, Hq, max_kv_splits, 128] / attn_lse [batch, Hq, max_kv_splits] (fp32,
+ * contiguous); empty splits write nothing.  Stage 2: out [batch, Hq, 128] (dtype,
+ * contiguous) = the LSE merge of each row's non-empty splits (0 for an empty row).  Query
+ * groups up to 4.
+ */
+int sgd_upstream_decode(const void *q, const void *k, const void *v, void *out, const int32_t *kv_indptr,
+                        const int32_t *kv_indices, float *attn_out, float *attn_lse, const int32_t *num_kv_splits,
+                        int32_t batch, int32_t max_kv_splits, int32_t query_heads, int32_t kv_heads,
+                        int32_t head_dim, const int64_t *q_strides, const int64_t *kv_strides, float scale,
+                        int32_t dtype, void *stream);
+
 /* Arguments of sgd_decode_noalloc: the inputs of one decode step and its output. */
 typedef struct sgd_noalloc_args {
     const void *q, *k, *v;          /* as in sgd_decode_args */
