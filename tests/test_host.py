@@ -332,3 +332,22 @@ def test_graph_update_checks_on_the_host():
         graph.update([q[:1]] * 2, [idx] * 2, [10, 30], [1, 1])
     with pytest.raises(RuntimeError, match="update"):
         graph.capture()
+
+
+def test_upstream_comparator_rejects_bad_arguments_before_launch():
+    """sgd_upstream_decode checks its geometry on the host (no GPU here): groups above 4,
+    head_dim other than 128, K/V strides that are not multiples of 8, unaligned K/V."""
+    from sglang_decode import _lib
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    qs = (ctypes.c_int64 * 3)(4096, 128, 1)
+    kvs = (ctypes.c_int64 * 4)(1024, 128, 1024, 128)
+
+    def call(hq=32, hkv=8, d=128, strides=kvs, k=fake, batch=4):
+        return lib.sgd_upstream_decode(fake, k, fake, fake, fake, fake, fake, fake, fake, batch, 16, hq, hkv, d, qs,
+                                       strides, ctypes.c_float(0.1), 0, None)
+    assert call(hq=64) == -22 and b"groups of up to 4" in lib.sgd_last_error()
+    assert call(d=64) == -22 and b"head_dim" in lib.sgd_last_error()
+    assert call(strides=(ctypes.c_int64 * 4)(1024, 127, 1024, 128)) == -22
+    assert call(k=ctypes.c_void_p((1 << 20) + 8)) == -22 and b"aligned" in lib.sgd_last_error()
+    assert call(batch=0) == 0  # nothing to do: no launch, no device access
