@@ -109,6 +109,13 @@ extern "C" int sgd_decode_noalloc(const sgd_noalloc_args *args, void *stream) {
     if (a.batch_capacity <= 0 || a.max_splits <= 0 || a.max_context <= 0 || a.query_heads <= 0 ||
         a.kv_heads <= 0 || a.head_dim <= 0 || a.workers <= 0)
         return einval("decode_noalloc: capacities, heads, head_dim and workers must be positive");
+    // bounds that keep the size arithmetic below exact (the plan and attention entries
+    // check the geometry in full)
+    if (a.batch_capacity > 4096 || (int64_t)a.batch_capacity * a.max_splits > 16384 || a.query_heads > 4096 ||
+        a.kv_heads > a.query_heads || a.head_dim > 256 || a.workers > 4096)
+        return einval("decode_noalloc: batch_capacity %d, max_splits %d, heads %d/%d, head_dim %d or workers %d "
+                      "beyond the planner's bounds", a.batch_capacity, a.max_splits, a.query_heads, a.kv_heads,
+                      a.head_dim, a.workers);
     constexpr int32_t kBlockKv = 128;
     const Layout L = layout_for(a.batch_capacity, a.max_splits, a.kv_heads, a.query_heads, a.head_dim, a.workers);
     if (L.total > kScratchBytes)

@@ -721,6 +721,7 @@ extern "C" int sgd_order_and_packs(const int32_t *weight, const int32_t *record_
     if (record_capacity <= 0 || record_capacity > kGreedyMaxRecords || kv_heads <= 0 || workers <= 0 ||
         buckets <= 0 || buckets > kMaxBuckets || rule_count < 0)
         return einval("order_and_packs: bad geometry");
+    if (force_mode < -1 || force_mode > 4) return einval("order_and_packs: force_mode %d outside [-1, 4]", force_mode);
     clear_stale_error();
     hipLaunchKernelGGL(k_order_and_packs, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, weight,
                        record_count, order, pack_first, pack_count, num_packs, mode, rules, rule_count,
@@ -747,6 +748,7 @@ int launch_build_plan(const sgd_plan_buffers *plan, int32_t force_mode, int32_t 
                       int32_t num_counters, const int32_t *kv_indptr, const int32_t *num_kv_splits, int32_t batch,
                       void *stream) {
     if (!plan) return einval("build_plan: null plan");
+    if (force_mode < -1 || force_mode > 4) return einval("build_plan: force_mode %d outside [-1, 4]", force_mode);
     if (int rc = check_plan_geometry(plan->batch_capacity, plan->max_splits, plan->kv_heads, plan->workers,
                                      plan->buckets))
         return rc;

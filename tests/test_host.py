@@ -293,6 +293,14 @@ def test_noalloc_rejects_geometry_beyond_its_scratch_before_any_device_call():
     assert lib.sgd_decode_noalloc(ctypes.byref(a), None) == -22
     msg = lib.sgd_last_error()
     assert b"needs" in msg and b"33554432" in msg
+    # capacities whose products would overflow the size arithmetic are refused by bound
+    for field, value in (("batch_capacity", 1 << 30), ("max_splits", 1 << 30), ("query_heads", 1 << 30),
+                         ("head_dim", 1 << 20), ("workers", 1 << 30), ("kv_heads", 64)):
+        saved = getattr(a, field)
+        setattr(a, field, value)
+        assert lib.sgd_decode_noalloc(ctypes.byref(a), None) == -22
+        assert b"beyond the planner's bounds" in lib.sgd_last_error()
+        setattr(a, field, saved)
     a.out = None
     assert lib.sgd_decode_noalloc(ctypes.byref(a), None) == -22
     assert b"null buffer" in lib.sgd_last_error()
@@ -351,3 +359,17 @@ def test_upstream_comparator_rejects_bad_arguments_before_launch():
     assert call(strides=(ctypes.c_int64 * 4)(1024, 127, 1024, 128)) == -22
     assert call(k=ctypes.c_void_p((1 << 20) + 8)) == -22 and b"aligned" in lib.sgd_last_error()
     assert call(batch=0) == 0  # nothing to do: no launch, no device access
+
+
+def test_plan_entries_reject_unknown_forced_modes():
+    """A forced mode outside R0..D4 is refused on the host (the device plan would otherwise
+    take it as a schedule id)."""
+    from sglang_decode import _lib
+    from sglang_decode.runtime.workspace import PlanBuffers
+    lib = _lib.lib()
+    plan = PlanBuffers(W.config_for("c1"), "cpu")
+    for bad in (-2, 5, 17):
+        assert lib.sgd_build_plan(ctypes.byref(plan.c_struct()), bad, 0, None, 0, None) == -22
+        assert b"force_mode" in lib.sgd_last_error()
+        assert lib.sgd_order_and_packs(None, None, None, None, None, None, None, None, 0, bad, 2, 8, 2, 64,
+                                       None) == -22
