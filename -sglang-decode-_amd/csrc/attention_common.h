@@ -107,28 +107,128 @@ __device__ __forceinline__ Unit unit_of(const sgd_decode_args &a, int32_t u, int
     return r;
 }
 
-// A claim the run hook makes itself (for_each_task<true>): in D1/D4 the hook of a
-// unit's last task takes the next unit while its last tiles stream -- one relaxed
-// atomic on `counter` by one thread -- and stores base + (old value) to `slot` (the
-// worker's LDS cursor) before the workgroup barrier that ends its task.  slot is null
-// for the other tasks and in the other modes.
-struct Preclaim {
-    int32_t *slot;
-    int32_t *counter;
-    int32_t base;
+// The start of a worker's next task, found by the run hook of for_each_task<true>
+// while the current task's last tiles stream, and left in LDS before the workgroup
+// barrier that ends the task: the claimed unit (`cursor`, D1/D4), `unit` and its entry
+// `e` when the next task opens a new unit (else unit -1), `task` and its record `info`
+// (task -1: nothing found).  Unit ids, entries and records do not change within a
+// launch, so a reader only matches the id.  Two of them alternate by task parity: the
+// hook of a worker's task k writes buffer (k + 1) & 1, which task k + 1 reads before
+// its own end barrier, and buffer k & 1 is not written again before task k + 1 has
+// passed that barrier -- no barrier is needed at a task's start.
+struct Prefetched {
+    int32_t cursor, unit, task;
+    Entry e;
+    TaskInfo info;
 };
 
-// Runs `run(task, info)` (PRECLAIM: `run(task, info, preclaim)`) for every task of this
-// worker, info being the task's record (from the dispatch table for a unit's first
+// What the run hook of for_each_task<true> is told.  `cur` is the buffer holding what
+// was found for this task; the hook fills buffer `next`.  When `claim` is set the hook
+// must take the worker's next unit -- one relaxed atomic on `counter` by one thread --
+// and store base + (old value) to pf[next].cursor before the task's end barrier.
+struct Successor {
+    Prefetched *pf;     // the two buffers
+    int32_t cur, next;
+    bool claim;         // D1/D4, last task of its unit
+    int32_t *counter;
+    int32_t base;
+    int32_t next_task;  // the unit's next task, or -1 when this task is the unit's last
+    int32_t next_unit;  // R0/R1/STATIC, last task of its unit: the worker's next unit (-1: none)
+    int32_t mode, limit;
+    bool table;         // units resolve through the dispatch table
+};
+
+__device__ __forceinline__ Entry uniform_entry(const Entry &e) {
+    auto f = [](int32_t v) { return __builtin_amdgcn_readfirstlane(v); };
+    return Entry{make_int4(f(e.x.x), f(e.x.y), f(e.x.z), f(e.x.w)), make_int4(f(e.y.x), f(e.y.y), f(e.y.z), f(e.y.w))};
+}
+
+__device__ __forceinline__ TaskInfo uniform_info(const TaskInfo &t) {
+    auto f = [](int32_t v) { return __builtin_amdgcn_readfirstlane(v); };
+    return TaskInfo{f(t.request), f(t.split), f(t.start), f(t.end), f(t.group)};
+}
+
+__device__ __forceinline__ TaskInfo entry_info(const Entry &e) {
+    return TaskInfo{e.x.z, e.x.w, e.y.x, e.y.y, e.y.z};
+}
+
+// Makes both prefetch buffers match nothing; all threads call it, before a barrier
+// that precedes for_each_task<true>.
+__device__ __forceinline__ void clear_prefetched(Prefetched *pf) {
+    if (threadIdx.x < 2) {
+        pf[threadIdx.x].unit = -1;
+        pf[threadIdx.x].task = -1;
+    }
+}
+
+// The hook's search for the worker's next task (run by one whole wave): the claim
+// (D1/D4), the dispatch entry or the record of the next task, and the page/slot indices
+// of its first kTokens tokens (0 past its end), all into s.pf[s.next] and idx[s.next].
+// `sh_indptr` (LDS, CSR) holds kv_indptr[0 .. iptr_n).
+template <bool CSR, int kTokens>
+__device__ __forceinline__ void prefetch_next(const sgd_decode_args &a, const Successor &s, int32_t (*idx)[kTokens],
+                                              int lane, int page_shift, const int32_t *sh_indptr, int32_t iptr_n) {
+    Prefetched &out = s.pf[s.next];
+    int32_t nt = s.next_task, nu = -1;
+    TaskInfo ni{};
+    Entry ne{};
+    bool opened = false;
+    if (nt >= 0) {
+        ni = decode_task(a, nt, s.mode);
+    } else {
+        nu = s.next_unit;
+        if (s.claim) {
+            int32_t c = 0;
+            if (lane == 0) c = __hip_atomic_fetch_add(s.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            nu = s.base + __builtin_amdgcn_readlane(c, 0);
+            if (lane == 0) out.cursor = nu;
+        }
+        if (s.table && nu >= 0 && nu < s.limit && nu < a.dispatch_units) {
+            ne = load_entry(a.dispatch, nu);
+            if (ne.y.w == table_kind(s.mode)) {
+                opened = true;
+                nt = ne.x.x;
+                ni = entry_info(ne);
+            }
+        }
+    }
+    nt = __builtin_amdgcn_readfirstlane(nt);
+    ni = uniform_info(ni);
+    if (nt >= 0) {
+        int32_t ind0 = 0;
+        if constexpr (CSR)
+            ind0 = __builtin_amdgcn_readfirstlane(ni.request < iptr_n ? sh_indptr[ni.request] : a.indptr[ni.request]);
+#pragma unroll
+        for (int j = lane; j < kTokens; j += 64) {
+            const int32_t tok = ni.start + j;
+            int32_t v = 0;
+            if (tok < ni.end) {
+                if constexpr (CSR) v = a.pages[ind0 + tok];
+                else v = a.pages[(int64_t)ni.request * a.pt_stride[0] + (int64_t)(tok >> page_shift) * a.pt_stride[1]];
+            }
+            idx[s.next][j] = v;
+        }
+    }
+    if (lane == 0) {
+        out.unit = opened ? nu : -1;
+        out.e = ne;
+        out.task = nt;
+        out.info = ni;
+    }
+}
+
+// Runs `run(task, info)` (PRECLAIM: `run(task, info, successor)`) for every task of
+// this worker, info being the task's record (from the dispatch table for a unit's first
 // task, else decode_task).  All threads of the workgroup execute it uniformly;
 // `sh_cursor` is one int of LDS.  In D1/D4 worker w runs pack w first and its claims
 // return workers + (counter): every pack still runs exactly once.  Without PRECLAIM the
 // next unit is taken when the current one is done (a claim made while a task is still
 // streaming most of its tiles holds work back from workers that free up first, and
-// measured slower); with it, the hook claims during its last tile rounds, so the claim
-// round trip overlaps them and the unit waits one round at most.
+// measured slower).  With it, the hook claims during the task's last tile rounds and
+// leaves the next task's entry and record in `pf` (two LDS buffers, cleared by
+// clear_prefetched), used instead of the table and record loads.
 template <bool PRECLAIM = false, class Run>
-__device__ void for_each_task(const sgd_decode_args &a, int32_t *sh_cursor, Run &&run) {
+__device__ void for_each_task(const sgd_decode_args &a, int32_t *sh_cursor, Run &&run, Prefetched *pf = nullptr) {
     const int32_t worker = blockIdx.x;
     const int32_t mode = __builtin_amdgcn_readfirstlane(*a.mode);
     const int32_t total = __builtin_amdgcn_readfirstlane(*a.record_count) * a.kv_heads;
@@ -146,28 +246,38 @@ __device__ void for_each_task(const sgd_decode_args &a, int32_t *sh_cursor, Run 
         return c;
     };
 
+    int32_t k = 0;  // tasks run so far; pf[k & 1] holds what was found for the next one
     int32_t unit = mode == 2 ? __builtin_amdgcn_readfirstlane(a.static_head[worker]) : worker;
     while (unit >= 0 && unit < limit) {
         const bool loaded = table && unit < a.dispatch_units;
         Entry e{};
-        if (loaded) e = load_entry(a.dispatch, unit);
-        const Unit u = unit_of(a, unit, mode, loaded, e);
-        for (int32_t i = 0; i < u.count; ++i) {
-            TaskInfo ti = (i == 0 && u.resolved) ? u.info : decode_task(a, u.first + i, mode);
-            ti.request = __builtin_amdgcn_readfirstlane(ti.request);
-            ti.split = __builtin_amdgcn_readfirstlane(ti.split);
-            ti.start = __builtin_amdgcn_readfirstlane(ti.start);
-            ti.end = __builtin_amdgcn_readfirstlane(ti.end);
-            ti.group = __builtin_amdgcn_readfirstlane(ti.group);
-            if constexpr (PRECLAIM)
-                run(u.first + i, ti, Preclaim{dynamic && i == u.count - 1 ? sh_cursor : nullptr, a.counter, claim_base});
-            else
-                run(u.first + i, ti);
+        if (loaded) {
+            if (PRECLAIM && __builtin_amdgcn_readfirstlane(pf[k & 1].unit) == unit) e = uniform_entry(pf[k & 1].e);
+            else e = load_entry(a.dispatch, unit);
         }
-        if (dynamic && PRECLAIM)  // the hook stored it before its task's last barrier; the next
-            unit = __builtin_amdgcn_readfirstlane(*sh_cursor);  // store follows the next task's first
+        const Unit u = unit_of(a, unit, mode, loaded, e);
+        const int32_t after = dynamic ? -1 : mode == 2 ? __builtin_amdgcn_readfirstlane(a.static_next[unit])
+                                                       : unit + a.workers;
+        for (int32_t i = 0; i < u.count; ++i, ++k) {
+            const int32_t task = u.first + i;
+            TaskInfo ti;
+            if (i == 0 && u.resolved) ti = u.info;
+            else if (PRECLAIM && __builtin_amdgcn_readfirstlane(pf[k & 1].task) == task) ti = pf[k & 1].info;
+            else ti = decode_task(a, task, mode);
+            ti = uniform_info(ti);
+            if constexpr (PRECLAIM) {
+                const bool last = i == u.count - 1;
+                run(task, ti,
+                    Successor{pf, k & 1, (k + 1) & 1, dynamic && last, a.counter, claim_base, last ? -1 : task + 1,
+                              !dynamic && last ? after : -1, mode, limit, table});
+            } else {
+                run(task, ti);
+            }
+        }
+        if (dynamic && PRECLAIM)  // the hook of the unit's last task stored it before that task's end barrier
+            unit = __builtin_amdgcn_readfirstlane(pf[k & 1].cursor);
         else
-            unit = dynamic ? claim() : mode == 2 ? __builtin_amdgcn_readfirstlane(a.static_next[unit]) : unit + a.workers;
+            unit = dynamic ? claim() : after;
     }
     // The last worker to finish puts the claim counter back to zero for the next
     // launch.  Relaxed is enough: a worker reaches this increment only after its

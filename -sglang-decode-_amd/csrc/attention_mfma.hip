@@ -31,7 +31,8 @@
 // registers, and at the end of the task the waves' (m, den, O) are merged through
 // LDS into the partial rows and natural-log LSEs of slot (request, head, split)
 // (kernels/attention.py:81-84).  Tasks and their order come from
-// attention_common.h's dispatch.
+// attention_common.h's dispatch; the last wave, once its tiles are done, claims and
+// looks up the worker's next task and the page/slot indices of its first tiles.
 #include "valu_ops.h"
 
 namespace sgd {
@@ -60,6 +61,8 @@ struct MfmaShared {
     float m[kWaves][kHeadsM];
     float d[kWaves][kHeadsM];
     int32_t cursor;
+    Prefetched pf[2];                    // the worker's next task (prefetch_next)
+    int32_t pf_idx[2][kTileT * kWaves];  // page/slot indices of its first kWaves tiles
 };
 
 template <int DT>
@@ -188,8 +191,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
     const int lane0 = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
     const int32_t G = a.query_heads / a.kv_heads;
     const float scale2 = a.scale * kLog2e;
+    const int page_shift = __builtin_ctz((unsigned)a.page_size);
+    clear_prefetched(sh.pf);
+    lds_barrier();
 
-    for_each_task(a, &sh.cursor, [&](int32_t, const TaskInfo &ti) {
+    for_each_task<true>(a, &sh.cursor, [&](int32_t task, const TaskInfo &ti, const Successor &succ) {
         // A laundered lane id per task: the compiler rebuilds the per-lane offsets
         // each task instead of holding them (64-bit each) live across the task loop.
         int lane = lane0;
@@ -206,10 +212,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
         t.kt = a.k_stride[1] * 2;
         t.vp = a.v_stride[0] * 2;
         t.vt = a.v_stride[1] * 2;
-        t.page_shift = __builtin_ctz((unsigned)a.page_size);
+        t.page_shift = page_shift;
         t.page_mask = a.page_size - 1;
         const int32_t ntiles = (t.end - t.start + kTileT - 1) / kTileT;
         const int32_t n0 = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
+        const bool prefetched = uni(sh.pf[succ.cur].task) == task;
 
         // q rows as the B operand: head n = lane % 16, dims 32c + 8j .. +7 (zero past G)
         uint4 q[4];
@@ -243,8 +250,10 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
         if (n0 > 0) {
             TileRegs cur, nxt;
             int32_t tile = wave;
-            tile_issue<CSR>(t, t.start + tile * kTileT, tile_index<CSR>(a, t, t.start + tile * kTileT, lane), lane,
-                            cur);
+            const int32_t idx0 = !prefetched              ? tile_index<CSR>(a, t, t.start + tile * kTileT, lane)
+                                 : lane < kTileT ? sh.pf_idx[succ.cur][wave * kTileT + lane]
+                                                 : 0;
+            tile_issue<CSR>(t, t.start + tile * kTileT, idx0, lane, cur);
             // indices of the wave's next tile (clamped to its last one)
             int32_t idx_next = tile_index<CSR>(a, t, t.start + min(tile + kWaves, ntiles - 1) * kTileT, lane);
             for (int32_t e = 0; e + 1 < n0; ++e) {
@@ -258,6 +267,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
             }
             tile_compute<DT>(cur, q, min(kTileT, t.end - (t.start + tile * kTileT)), scale2, lane, m_l, den_l, o);
         }
+
+        // The last wave holds the fewest tiles (round-robin deal): once they are done it
+        // finds the worker's next task, so those round trips overlap the other waves'
+        // last tiles; the barrier below publishes it.
+        if (wave == kWaves - 1) prefetch_next<CSR, kTileT * kWaves>(a, succ, sh.pf_idx, lane, page_shift, nullptr, 0);
 
         // wave state to LDS: head n = lane % 16, dims 32j + 8i + b
         den_l += __shfl_xor(den_l, 16, 64);
@@ -293,7 +307,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
             a.partial[slot * kD + d] = acc / dd;
             if (d == 0) a.lse[slot] = (mm + __log2f(dd)) * kLn2;
         }
-    });
+    }, sh.pf);
 }
 
 template <int DT, bool CSR>

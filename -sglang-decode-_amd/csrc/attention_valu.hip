@@ -38,6 +38,8 @@ struct ValuShared {
     float cd[kWaves][kHeads];
     int32_t indptr[kIndptrLds];
     int32_t cursor;
+    Prefetched pf[2];                   // the worker's next task (prefetch_next)
+    int32_t pf_idx[2][kTile * kWaves];  // page/slot indices of its first kWaves tiles
 };
 
 // ------------------------------------------------------------------ kernel
@@ -60,10 +62,11 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
     if constexpr (CSR) {
         iptr_n = min(__builtin_amdgcn_readfirstlane(*a.active) + 1, kIndptrLds);
         for (int i = threadIdx.x; i < iptr_n; i += 64 * kWaves) sh.indptr[i] = a.indptr[i];
-        lds_barrier();
     }
+    clear_prefetched(sh.pf);
+    lds_barrier();
 
-    for_each_task<true>(a, &sh.cursor, [&](int32_t, const TaskInfo &ti, const Preclaim &pc) {
+    for_each_task<true>(a, &sh.cursor, [&](int32_t task, const TaskInfo &ti, const Successor &succ) {
         int lane = lane0;  // laundered per task: per-lane offsets are rebuilt, not held live
         asm volatile("" : "+v"(lane));
         // Global loads first -- q rows (wave 0), then the request's index base, the first
@@ -96,10 +99,17 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
         T.vt = a.v_stride[1] * 2;
         const int32_t ntiles = (T.end - T.start + kTile - 1) / kTile;
         const int32_t n0 = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
+        const bool prefetched = uni(sh.pf[succ.cur].task) == task;
         uint4 kr[kRowsLoads], vr[kRowsLoads];
         int32_t idx_next = 0;
         if (n0 > 0) {
-            const int32_t i0 = tile_index<CSR>(a, T, T.start + wave * kTile, lane, page_shift);
+            int32_t i0;
+            if (prefetched) {
+                const int i = lane & 15;
+                i0 = i < kRowsLoads ? sh.pf_idx[succ.cur][wave * kTile + 4 * i + (lane >> 4)] : 0;
+            } else {
+                i0 = tile_index<CSR>(a, T, T.start + wave * kTile, lane, page_shift);
+            }
             tile_issue<CSR>(T, wave, i0, page_mask, lane, kr, vr);
             if (n0 > 1) idx_next = tile_index<CSR>(a, T, T.start + (wave + kWaves) * kTile, lane, page_shift);
         }
@@ -129,11 +139,11 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
         }
 
         // ---- end of the wave's tiles.  The last wave has the fewest tiles (round-robin
-        // deal): with none of its loads in flight, it takes the worker's next unit now, so
-        // the claim's round trip overlaps the other waves' last tiles; the merge barrier
-        // below publishes it to for_each_task.
-        if (pc.slot != nullptr && wave == kWaves - 1 && lane0 == 0)
-            *pc.slot = pc.base + __hip_atomic_fetch_add(pc.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // deal): with none of its loads in flight, it finds the worker's next task now;
+        // the merge barrier below publishes it to for_each_task and to the next task's
+        // first tile issue.
+        if (wave == kWaves - 1)
+            prefetch_next<CSR, kTile * kWaves>(a, succ, sh.pf_idx, lane, page_shift, sh.indptr, iptr_n);
         // ---- reduce within the wave, then merge the waves
         const Roles ro(lane);
         float mh[kHeads], dh[kHeads];
@@ -176,7 +186,7 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
                 if (d == 0) a.lse[slot] = (mm + __log2f(dd)) * kLn2;
             }
         }
-    });
+    }, sh.pf);
 }
 
 template <int DT, bool CSR, int kWaves>

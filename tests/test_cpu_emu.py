@@ -75,6 +75,19 @@ def test_small_batch_every_mode_and_kernel(asan_build):
         _assert_clean(rc, rows, err, len(kernels) * len(modes))
 
 
+def test_few_workers_walk_long_task_chains(asan_build):
+    """3 to 5 workers, so every worker runs many tasks in a row: the next-task search that
+    the last wave of the valu and mfma kernels makes while the other waves finish (the
+    claim, the entry or record, the first tiles' page/slot indices, left in LDS by task
+    parity) is taken on every task boundary -- new units and packs of several tasks,
+    CSR and paged, every schedule -- in bounds and against the oracle."""
+    cases = [{"workload": "c1", "workers": 3, "kernels": ["valu", "mfma"], "modes": [0, 1, 2, 3, 4]},
+             {"workload": "c4", "workers": 5, "requests": 1, "kernels": ["mfma"], "modes": [4]},
+             {"workload": "c2", "workers": 5, "requests": 2, "kernels": ["valu"], "modes": [3]}]
+    rc, rows, err = _run(cases)
+    _assert_clean(rc, rows, err, 10 + 1 + 1)
+
+
 def test_executor_reports_out_of_bounds(asan_build):
     """The harness itself: an output buffer one row short makes the merge store past it,
     and the run aborts with AddressSanitizer's report naming the kernel."""
