@@ -19,7 +19,9 @@
 // the index load of the tile after it are in flight while a tile is computed.
 // At the end of a task the waves' (m, den, acc) are merged through LDS, and the
 // normalized partial and natural-log LSE go to slot (request, head, split)
-// (kernels/attention.py:81-84).
+// (kernels/attention.py:81-84).  The last wave, which holds the fewest tiles, finds
+// the worker's next task (claim, dispatch entry or record, the first tiles' page/slot
+// indices) once its own tiles are done, while the others finish theirs.
 //
 #include "valu_ops.h"
 
