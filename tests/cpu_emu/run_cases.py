@@ -9,6 +9,13 @@ kernel that takes its shape), or {"workload": "c1".."c5", "modes": [...], "kerne
 JSON line per (case, kernel, mode) goes to stdout: violations of the 2e-2 abs / 1e-2 rel
 tolerance, NaNs, nonzero rows past the batch, the plan compared bit-exactly with the
 oracle, and the claim counters left at zero.
+
+Two more case kinds drive the entry points outside the engine's path:
+{"upstream": [lengths, max_splits], "dtype": ...} runs the upstream two-stage comparator
+(sgd_upstream_decode) and checks its output and every non-empty split slot against the
+oracle; {"noalloc": workload, "batches": [[n, shrink], ...], "mode": m} runs
+sgd_decode_noalloc on consecutive calls (the first n requests, contexts divided by
+shrink) and compares each bitwise with the allocating entry points on the same inputs.
 """
 import json
 import os
@@ -115,6 +122,101 @@ def _lpt_trials(emu, trials, seed):
     return dict(case="lpt", trials=trials, mismatches=len(bad), first=bad[:3])
 
 
+def _upstream(emu, lengths, smax, dtype):
+    import ctypes
+    import numpy as np
+    import driver as D
+    from oracle import attention as OA
+    from sglang_decode import _lib
+    from sglang_decode import workloads as W
+    from sglang_decode.config import DecodeConfig
+    from sglang_decode.planning.reference import split_records
+    import torch
+    c = DecodeConfig(batch_capacity=len(lengths), max_splits=smax, max_context=max(4096, max(lengths)),
+                     query_heads=8, kv_heads=2, page_size=1, workers=8)
+    q, k, v, indptr, indices = W.make_csr_inputs(c, lengths, seed=len(lengths), device="cpu", dtype=dtype)
+    splits = W.split_hints(lengths, smax)
+    b, hq, d = len(lengths), c.query_heads, c.head_dim
+    dt = _lib.dtype_code(dtype)
+    qd, kd, vd = emu.upload(D.bits16(q)), emu.upload(D.bits16(k)), emu.upload(D.bits16(v))
+    ipd = emu.upload(indptr.numpy().astype(np.int32)[:b + 1])
+    idd = emu.upload(indices.numpy().astype(np.int32))
+    sd = emu.upload(np.array(splits, np.int32))
+    slots = emu.array((b, hq, smax, d), np.float32, np.nan)
+    slse = emu.array((b, hq, smax), np.float32, np.nan)
+    out = emu.array((b, hq, d), np.uint16)
+    qs = (ctypes.c_int64 * 3)(*q.stride())
+    kvs = (ctypes.c_int64 * 4)(k.stride(0), k.stride(1), v.stride(0), v.stride(1))
+    emu.check(emu.lib.sgd_upstream_decode(D.ptr(qd), D.ptr(kd), D.ptr(vd), D.ptr(out), D.ptr(ipd), D.ptr(idd),
+                                          D.ptr(slots), D.ptr(slse), D.ptr(sd), b, smax, hq, c.kv_heads, d, qs, kvs,
+                                          ctypes.c_float(d ** -0.5), dt, None), "upstream_decode")
+    got = D.from_bits16(out, dt).reshape(out.shape)
+    exp = OA.csr_attention(q, k, v, indptr, indices, lengths)[:b]
+    viol = int((np.abs(got - exp) > 2e-2 + 1e-2 * np.abs(exp)).sum())
+    records, _, _ = split_records(lengths, splits, c)
+    table = torch.zeros((b, max(max(lengths), 1)), dtype=torch.int32)
+    for r, n in enumerate(lengths):
+        table[r, :n] = indices[int(indptr[r]):int(indptr[r]) + n]
+    ref = OA.split_partials(q, k[:, None], v[:, None], table, lengths, 1,
+                            [(x.request, x.split, x.begin, x.end) for x in records], hq, smax)
+    slot_viol = 0
+    for (r, h, s), (p, l) in ref.items():
+        slot_viol += int((np.abs(slots[r, h, s] - p) > 2e-2 + 1e-2 * np.abs(p)).sum())
+        slot_viol += int(abs(slse[r, h, s] - l) > 1e-2 + 1e-3 * abs(l))
+    return dict(case="upstream", lengths=lengths, smax=smax, dtype=str(dtype), violations=viol,
+                slot_violations=slot_viol, slots=len(ref), nans=int(np.isnan(got).sum()))
+
+
+def _noalloc(emu, name, batches, mode, dtype):
+    import ctypes
+    import numpy as np
+    import driver as D
+    from oracle import attention as OA
+    from sglang_decode import _lib
+    from sglang_decode import workloads as W
+    c = W.config_for(name, workers=64)
+    full = W.lengths_for(name)
+    out = emu.array((c.batch_capacity, c.query_heads, c.head_dim), np.uint16, 0x7fc0)
+    rows = []
+    for n, shrink in batches:
+        lengths = [max(1, x // shrink) for x in full[:n]]
+        splits = W.split_hints(lengths, c.max_splits)
+        csr = c.page_size == 1
+        inputs, oracle = _inputs(c, lengths, csr, 70 + n, dtype)
+        q, k, v, pages, indptr = inputs
+        ref = D.decode(emu, c, lengths, splits, q, k, v, pages, indptr, mode=mode)
+        L = emu.array((c.batch_capacity,), np.int32, 0)
+        S = emu.array((c.batch_capacity,), np.int32, 1)
+        L[:n], S[:n] = lengths, splits
+        A = emu.upload(np.array([n], np.int32))
+        qd, kd, vd = emu.upload(D.bits16(q)), emu.upload(D.bits16(k)), emu.upload(D.bits16(v))
+        pd = emu.upload(pages.numpy().astype(np.int32))
+        ipd = emu.upload(indptr.numpy().astype(np.int32)) if csr else None
+        a = _lib.NoAllocArgsC()
+        a.q, a.k, a.v, a.pages = qd.ctypes.data, kd.ctypes.data, vd.ctypes.data, pd.ctypes.data
+        a.indptr = ipd.ctypes.data if csr else None
+        a.lengths, a.splits, a.active, a.out = L.ctypes.data, S.ctypes.data, A.ctypes.data, out.ctypes.data
+        a.scale = float(c.head_dim ** -0.5)
+        a.q_stride[:] = list(q.stride())
+        if csr:
+            a.k_stride[:] = [k.stride(0), 0, k.stride(1), k.stride(2)]
+            a.v_stride[:] = [v.stride(0), 0, v.stride(1), v.stride(2)]
+            a.pt_stride[:] = [0, 0]
+        else:
+            a.k_stride[:], a.v_stride[:], a.pt_stride[:] = list(k.stride()), list(v.stride()), list(pages.stride())
+        a.batch_capacity, a.max_splits, a.max_context = c.batch_capacity, c.max_splits, c.max_context
+        a.query_heads, a.kv_heads, a.head_dim = c.query_heads, c.kv_heads, c.head_dim
+        a.page_size, a.csr, a.dtype, a.workers = c.page_size, int(csr), _lib.dtype_code(dtype), c.workers
+        a.force_mode, a.kernel = int(mode), _lib.KERNELS["auto"]
+        emu.check(emu.lib.sgd_decode_noalloc(ctypes.byref(a), None), "decode_noalloc")
+        got = D.from_bits16(out, a.dtype).reshape(out.shape)
+        exp = oracle(None)[:n]
+        rows.append(dict(batch=n, bitwise=bool(np.array_equal(got, ref["out"], equal_nan=True)),
+                         violations=int((np.abs(got[:n] - exp) > 2e-2 + 1e-2 * np.abs(exp)).sum()),
+                         tail=float(np.abs(got[n:]).sum())))
+    return dict(case="noalloc", workload=name, mode=int(mode), calls=rows)
+
+
 def run(cases, asan):
     import torch
     import driver as D
@@ -123,6 +225,13 @@ def run(cases, asan):
     for case in cases:
         if "lpt" in case:
             print(json.dumps(_lpt_trials(emu, int(case["lpt"]), int(case.get("seed", 0)))), flush=True)
+        elif "upstream" in case:
+            lengths, smax = case["upstream"]
+            print(json.dumps(_upstream(emu, list(lengths), int(smax), getattr(torch, case.get("dtype", "bfloat16")))),
+                  flush=True)
+        elif "noalloc" in case:
+            print(json.dumps(_noalloc(emu, case["noalloc"], case["batches"], int(case.get("mode", -1)),
+                                      getattr(torch, case.get("dtype", "bfloat16")))), flush=True)
         elif "sweep" in case:
             from test_gpu_sweep import draw, kernels_for
             seed = int(case["sweep"])

@@ -17,6 +17,8 @@ What this pins:
 * The held sweep draws and the long-task draws run in bounds on every kernel that takes
   their shape, match the FP32 oracle (2e-2 abs / 1e-2 rel), build the oracle's plan
   bit-exactly and leave the claim counters at zero.
+* The entry points outside the engine's path -- the upstream comparator and the
+  no-allocation entry with its static device array -- run in bounds as well.
 """
 import json
 import os
@@ -86,6 +88,32 @@ def test_few_workers_walk_long_task_chains(asan_build):
              {"workload": "c2", "workers": 5, "requests": 2, "kernels": ["valu"], "modes": [3]}]
     rc, rows, err = _run(cases)
     _assert_clean(rc, rows, err, 10 + 1 + 1)
+
+
+def test_upstream_comparator_and_no_alloc_entry_in_bounds(asan_build):
+    """The two entry points outside the engine's path.  sgd_upstream_decode (the upstream
+    two-stage split-KV comparator): empty, 1-token and 700-token rows over 16 splits, a
+    3000-token row over 4 (fp16), equal rows with one split -- output and every non-empty
+    split slot against the oracle.  sgd_decode_noalloc (plan tables, counters and split
+    slots in the library's static array): two calls in a row, the second smaller, CSR (D1)
+    and paged group 8 (D4), each bitwise equal to the allocating entry points."""
+    cases = [{"upstream": [[0, 1, 17, 33, 257, 513, 700], 16]},
+             {"upstream": [[3000, 5, 129], 4], "dtype": "float16"},
+             {"upstream": [[64] * 5, 1]},
+             {"noalloc": "c1", "batches": [[4, 1], [2, 3]], "mode": 3},
+             {"noalloc": "c4", "batches": [[2, 16], [1, 32]], "mode": 4}]
+    rc, rows, err = _run(cases)
+    assert rc == 0, f"executor run failed (rc {rc}):\n{err[-4000:]}"
+    assert "ERROR: AddressSanitizer" not in err, err[-4000:]
+    assert len(rows) == len(cases), (len(rows), err[-2000:])
+    for r in rows:
+        if r["case"] == "upstream":
+            assert r["violations"] == 0 and r["slot_violations"] == 0 and r["nans"] == 0, r
+            assert r["slots"] > 0, r
+        else:
+            assert len(r["calls"]) == 2, r
+            for call in r["calls"]:
+                assert call["bitwise"] and call["violations"] == 0 and call["tail"] == 0.0, r
 
 
 def test_executor_reports_out_of_bounds(asan_build):
