@@ -113,9 +113,10 @@ __device__ __forceinline__ Unit unit_of(const sgd_decode_args &a, int32_t u, int
 // `e` when the next task opens a new unit (else unit -1), `task` and its record `info`
 // (task -1: nothing found).  Unit ids, entries and records do not change within a
 // launch, so a reader only matches the id.  Two of them alternate by task parity: the
-// hook of a worker's task k writes buffer (k + 1) & 1, which task k + 1 reads before
-// its own end barrier, and buffer k & 1 is not written again before task k + 1 has
-// passed that barrier -- no barrier is needed at a task's start.
+// hook of a worker's task k fills buffer (k + 1) & 1 before task k's end barrier; it is
+// read after that barrier, up to task k + 1's end barrier, and written next by the hook
+// of task k + 2, which runs only after task k + 1's end barrier -- so no barrier is
+// needed at a task's start.
 struct Prefetched {
     int32_t cursor, unit, task;
     Entry e;
