@@ -159,8 +159,6 @@ extern "C" int sgd_decode_noalloc(const sgd_noalloc_args *args, void *stream) {
     p.workers = a.workers;
     p.block_kv = kBlockKv;
     p.buckets = buckets_for(a.max_context, kBlockKv);
-    if (int rc = sgd_build_plan(&p, a.force_mode, a.force_mode == 2, sync, 2, stream)) return rc;
-
     sgd_decode_args d{};
     d.q = a.q;
     d.k = a.k;
@@ -203,6 +201,10 @@ extern "C" int sgd_decode_noalloc(const sgd_noalloc_args *args, void *stream) {
     d.dtype = a.dtype;
     d.workers = a.workers;
     d.kernel = a.kernel;
+    // Every refusal happens before the first device call: the attention's geometry and
+    // kernel checks (the plan entry checks its own arguments before it launches).
+    if (const int rc = sgd_attention_kernel(&d); rc < 0) return rc;
+    if (int rc = sgd_build_plan(&p, a.force_mode, a.force_mode == 2, sync, 2, stream)) return rc;
     if (int rc = sgd_persistent_decode(&d, stream)) return rc;
     return sgd_merge_splits(d.partial, d.lse, p.counts, a.active, p.error, a.out, a.batch_capacity,
                             a.query_heads, a.head_dim, a.max_splits, a.dtype, stream);

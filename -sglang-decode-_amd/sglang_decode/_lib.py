@@ -67,6 +67,7 @@ _SIGNATURES = {
     "sgd_attention_kernel": (_I, [ctypes.POINTER(DecodeArgsC)]),
     "sgd_merge_splits": (_I, [_P] * 6 + [_I] * 5 + [_P]),
     "sgd_host_static_lists": (_I, [_P, _I, _I, _I, _I, _P, _P]),
+    "sgd_host_static_plan": (_I, [_P, _P] + [_I] * 7 + [_P, _P, _P]),
     "sgd_decode_noalloc": (_I, [ctypes.POINTER(NoAllocArgsC), _P]),
     "sgd_upstream_decode": (_I, [_P] * 9 + [_I] * 5 + [_P, _P, ctypes.c_float, _I, _P]),
     "sgd_store_kv_stage_q": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, ctypes.c_int64, _P, _P, _P, _P,

@@ -17,11 +17,21 @@ def decode_attention_fwd(q, k_buffer, v_buffer, o, kv_indptr, kv_indices, attn_l
     kv_indptr int32 [batch + 1], kv_indices int32, num_kv_splits int32 [batch];
     attn_logits fp32 [batch, Hq, max_kv_splits, D] and attn_lse fp32 [batch, Hq,
     max_kv_splits] (contiguous) receive the split partials and LSEs."""
+    if q.ndim != 3 or k_buffer.ndim != 3 or v_buffer.shape != k_buffer.shape:
+        raise ValueError("decode_attention_fwd: q must be [batch, Hq, D] and k_buffer / v_buffer one "
+                         "[tokens, Hkv, D] shape")
     batch, hq, d = q.shape
     hkv = k_buffer.shape[1]
-    for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices), ("num_kv_splits", num_kv_splits)):
-        if t.dtype != torch.int32 or not t.is_contiguous():
-            raise ValueError(f"decode_attention_fwd: {name} must be contiguous int32")
+    if k_buffer.shape[2] != d or (k_buffer.dtype, v_buffer.dtype) != (q.dtype, q.dtype):
+        raise ValueError("decode_attention_fwd: k_buffer / v_buffer must match q's head_dim and dtype")
+    tensors = (q, k_buffer, v_buffer, o, kv_indptr, kv_indices, attn_logits, attn_lse, num_kv_splits)
+    if any(t.device != q.device for t in tensors):
+        raise ValueError("decode_attention_fwd: every tensor must be on q's device")
+    # both stages read kv_indptr[b + 1] and num_kv_splits[b] for every b < batch
+    for name, t, n in (("kv_indptr", kv_indptr, batch + 1), ("kv_indices", kv_indices, 0),
+                       ("num_kv_splits", num_kv_splits, batch)):
+        if t.dtype != torch.int32 or not t.is_contiguous() or t.numel() < n:
+            raise ValueError(f"decode_attention_fwd: {name} must be contiguous int32 with at least {n} entries")
     if (tuple(attn_logits.shape) != (batch, hq, max_kv_splits, d) or tuple(attn_lse.shape) != (batch, hq, max_kv_splits)
             or not (attn_logits.is_contiguous() and attn_lse.is_contiguous())):
         raise ValueError("decode_attention_fwd: attn_logits / attn_lse must be contiguous [batch, Hq, max_kv_splits"

@@ -1,23 +1,24 @@
-"""Offline calibration gate: freeze one bounded policy rule from two independent sets of
-measured samples (calibration and holdout); runs no kernel.
+"""Policy calibration gate: turns two independent sets of measured step times into at
+most one validated policy rule.  No kernel runs here.
 
-Behaviour of scripts/calibrate_policy.py:10-59:
-* a samples CSV has rows ``variant, wall_us, status`` (``bench.py --samples-csv`` writes
-  them; extra columns are ignored).  Any row whose status is not ``ok`` is an error --
-  failed samples are investigated, never dropped -- and each of R1, STATIC_CPU, D1, D4
-  needs at least five samples;
-* the candidate is the variant with the lowest median on the calibration set.  A dynamic
-  candidate (D1/D4) must beat the better static variant (R1 or STATIC_CPU) by at least
-  3% in median and with no overlap (its slowest sample faster than the static's
-  fastest), else the static variant is taken;
-* on the holdout set the candidate may not be more than 2% slower than the better
-  static variant, and a dynamic candidate must be at least 3% faster there, again with no
-  overlap -- otherwise nothing is published;
-* a host-static (STATIC_CPU) winner is kept as the baseline and no rule is published for
-  it (the device LPT is not substituted for it in AUTO);
-* the artifact ``{"status": "validated", "evidence": [{path, sha256} x 2], "rules":
-  [{min_tasks, max_tasks, min_ratio, max_ratio, mode}]}`` is created, never overwritten,
-  and loads with ``planning.policy.load_policy``.
+The decision rules are the reference's (scripts/calibrate_policy.py:10-59); the code
+and messages are this package's:
+
+* Inputs are two CSV files (calibration, holdout) with columns ``variant``, ``wall_us``
+  and ``status`` (``bench.py --samples-csv`` writes them; other columns are ignored).
+  A row whose status is not ``ok`` stops the gate, and every schedule of the gate
+  (R1, STATIC_CPU, D1, D4) needs five or more samples in each file.
+* The pick is the schedule with the lowest calibration median.  A dynamic pick (D1/D4)
+  stands only if it clears the bar against the better static schedule (R1 or
+  STATIC_CPU): a median at least 3% lower and every sample below the static one's
+  fastest.  Otherwise the static schedule is the pick.
+* On the holdout set the pick may be at most 2% slower than the better static schedule
+  there, and a dynamic pick must clear the same bar again; else nothing is published.
+* A host-LPT pick (STATIC_CPU) is never published: it stays the baseline, and the device
+  LPT is not put in its place.
+* The artifact -- ``{"status": "validated", "evidence": [{path, sha256}, ...], "rules":
+  [{min_tasks, max_tasks, min_ratio, max_ratio, mode}]}`` -- is written only to a path
+  that does not exist yet, and ``planning.policy.load_policy`` reads it.
 
 Usage: ``python -m sglang_decode.planning.calibrate CAL.csv HOLDOUT.csv --output
 policy.json --tasks MIN MAX --ratio MIN MAX``.
@@ -29,62 +30,83 @@ import json
 import statistics
 from pathlib import Path
 
-MODES = {"R1": 1, "STATIC_CPU": 2, "D1": 3, "D4": 4}
+from ..config import Mode
+
+# Sample names of the gate and the device mode each one publishes.
+SCHEDULES = {"R1": Mode.R1, "STATIC_CPU": Mode.STATIC, "D1": Mode.D1, "D4": Mode.D4}
 STATIC = ("R1", "STATIC_CPU")
+MIN_SAMPLES = 5
+DYNAMIC_GAIN = 0.03      # a dynamic schedule's median must be this much below the static one
+HOLDOUT_SLACK = 0.02     # how much slower than the best static schedule the pick may be on the holdout
 
 
 class GateRejected(Exception):
     """The measurements do not support publishing a rule."""
 
 
-def read_samples(path):
-    groups = {}
-    with Path(path).open(newline="") as f:
-        for row in csv.DictReader(f):
-            if row["status"] != "ok":
-                raise ValueError("failed samples need investigation; do not silently drop them")
-            groups.setdefault(row["variant"], []).append(float(row["wall_us"]))
-    for name in MODES:
-        if len(groups.get(name, [])) < 5:
-            raise ValueError(f"at least five full-wall rounds required for {name}")
-    return groups
+class Samples:
+    """Step times per schedule from one CSV file."""
+
+    def __init__(self, path):
+        self.path = Path(path)
+        self.times = {}
+        with self.path.open(newline="") as f:
+            for line, row in enumerate(csv.DictReader(f), start=2):
+                if row["status"] != "ok":
+                    raise ValueError(f"{self.path}:{line}: sample status {row['status']!r}; a failed "
+                                     "measurement has to be explained, not filtered out")
+                self.times.setdefault(row["variant"], []).append(float(row["wall_us"]))
+        short = [f"{name} ({len(self.times.get(name, []))})" for name in SCHEDULES
+                 if len(self.times.get(name, [])) < MIN_SAMPLES]
+        if short:
+            raise ValueError(f"{self.path}: the gate needs at least {MIN_SAMPLES} samples per schedule; "
+                             f"too few for {', '.join(short)}")
+
+    def median(self, name):
+        return statistics.median(self.times[name])
+
+    def fastest(self, names):
+        return min(names, key=self.median)
+
+    def clears(self, dynamic, static):
+        """True when ``dynamic`` beats ``static`` by the adoption bar: a median at least
+        DYNAMIC_GAIN lower and no overlap (its slowest sample below the static's fastest)."""
+        gain = 1.0 - self.median(dynamic) / self.median(static)
+        return gain >= DYNAMIC_GAIN and max(self.times[dynamic]) < min(self.times[static])
 
 
-def _median(groups, name):
-    return statistics.median(groups[name])
-
-
-def choose(calibration, holdout):
-    """The variant the gate publishes (R1, D1 or D4); GateRejected when there is none."""
-    static = min(STATIC, key=lambda n: _median(calibration, n))
-    candidate = min(MODES, key=lambda n: _median(calibration, n))
-    if candidate in ("D1", "D4"):
-        gain = 1 - _median(calibration, candidate) / _median(calibration, static)
-        if gain < 0.03 or max(calibration[candidate]) >= min(calibration[static]):
-            candidate = static
-    hold_static = min(STATIC, key=lambda n: _median(holdout, n))
-    if _median(holdout, candidate) > 1.02 * _median(holdout, hold_static):
-        raise GateRejected("holdout regression exceeds 2%; no policy published")
-    if candidate in ("D1", "D4") and (_median(holdout, candidate) > 0.97 * _median(holdout, hold_static)
-                                      or max(holdout[candidate]) >= min(holdout[hold_static])):
-        raise GateRejected("dynamic holdout benefit is below the adoption gate")
-    if candidate == "STATIC_CPU":
-        raise GateRejected("host static wins: retain it as baseline; do not substitute GPU LPT in AUTO")
-    return candidate
+def choose(calibration: Samples, holdout: Samples):
+    """The schedule the gate publishes (R1, D1 or D4); GateRejected when there is none."""
+    base = calibration.fastest(STATIC)
+    pick = calibration.fastest(SCHEDULES)
+    if pick not in STATIC and not calibration.clears(pick, base):
+        pick = base
+    hold_base = holdout.fastest(STATIC)
+    if holdout.median(pick) > (1.0 + HOLDOUT_SLACK) * holdout.median(hold_base):
+        raise GateRejected(f"{pick} is more than 2% slower than {hold_base} on the holdout set; "
+                           "no rule published")
+    if pick not in STATIC and not holdout.clears(pick, hold_base):
+        raise GateRejected(f"{pick} does not repeat its gain over {hold_base} on the holdout set; "
+                           "no rule published")
+    if pick == "STATIC_CPU":
+        raise GateRejected("the host LPT is fastest: it stays the baseline and "
+                           "no device rule replaces it")
+    return pick
 
 
 def calibrate(calibration_path, holdout_path, output, tasks, ratio):
     """Writes the validated artifact to ``output`` (which must not exist) and returns it."""
-    calibration_path, holdout_path, output = Path(calibration_path), Path(holdout_path), Path(output)
-    if calibration_path.resolve() == holdout_path.resolve():
-        raise ValueError("independent holdout artifact required")
-    candidate = choose(read_samples(calibration_path), read_samples(holdout_path))
-    evidence = [dict(path=str(p), sha256=hashlib.sha256(p.read_bytes()).hexdigest())
-                for p in (calibration_path, holdout_path)]
-    artifact = dict(status="validated", evidence=evidence,
-                    rules=[dict(min_tasks=int(tasks[0]), max_tasks=int(tasks[1]), min_ratio=int(ratio[0]),
-                                max_ratio=int(ratio[1]), mode=MODES[candidate])])
-    with output.open("x") as f:
+    cal_path, hold_path, output = Path(calibration_path), Path(holdout_path), Path(output)
+    if cal_path.resolve() == hold_path.resolve():
+        raise ValueError("the holdout set must be an independent file, not the calibration set")
+    pick = choose(Samples(cal_path), Samples(hold_path))
+    rule = dict(min_tasks=int(tasks[0]), max_tasks=int(tasks[1]), min_ratio=int(ratio[0]),
+                max_ratio=int(ratio[1]), mode=int(SCHEDULES[pick]))
+    artifact = dict(status="validated",
+                    evidence=[dict(path=str(p), sha256=hashlib.sha256(p.read_bytes()).hexdigest())
+                              for p in (cal_path, hold_path)],
+                    rules=[rule])
+    with output.open("x") as f:  # never replace an existing artifact
         json.dump(artifact, f, indent=2)
     return artifact
 
@@ -94,8 +116,8 @@ def main(argv=None):
     ap.add_argument("calibration", type=Path)
     ap.add_argument("holdout", type=Path)
     ap.add_argument("--output", type=Path, required=True)
-    ap.add_argument("--tasks", nargs=2, type=int, required=True)
-    ap.add_argument("--ratio", nargs=2, type=int, required=True)
+    ap.add_argument("--tasks", nargs=2, type=int, required=True, metavar=("MIN", "MAX"))
+    ap.add_argument("--ratio", nargs=2, type=int, required=True, metavar=("MIN", "MAX"))
     args = ap.parse_args(argv)
     try:
         calibrate(args.calibration, args.holdout, args.output, args.tasks, args.ratio)

@@ -98,6 +98,11 @@ def parse():
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="also run a plain N-MiB read+write kernel 5 times, so a rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE pass can scale its counts to bytes")
+    ap.add_argument("--head-dim", type=int, default=0, choices=(0, 64, 128, 256),
+                    help="override the workload's head_dim (0 = its own, 128): the same batch, heads and "
+                         "contexts at head_dim 64 or 256")
+    ap.add_argument("--no-reference-b", action="store_true",
+                    help="skip the reference's published workload B (eager single-layer entries per schedule)")
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "traffic_persistent_decode.json"),
                     help="measured HBM bytes per attention launch (from rocprofv3 --pmc), used for "
                          "roofline.traffic when kernel, schedule and workers match this run")
@@ -240,6 +245,125 @@ def time_plan_inputs(c, lengths, splits, dev, reps=32, rounds=5):
     return out
 
 
+# The reference's one published workload (benchmarks/workloads.py:7, workload B) and its
+# figure, taken from the author's earlier materials on unstated hardware (A100 inferred from
+# configs/a100_bf16.json) and not re-measured there (docs/resume_mapping.md:26).
+REFERENCE_B = [256] * 24 + [1536] * 4 + [16384] * 4
+REFERENCE_B_PUBLISHED = dict(R0_us=237.0, D4_us=214.0, hardware="not stated (A100 inferred)",
+                             source="docs/resume_mapping.md:26",
+                             note="history from other hardware, not re-measured by the reference; not a target")
+
+
+def time_reference_workload_b(dev, dtype, worker_counts, iterations, rounds, threads):
+    """Workload B at the reference's own boundary (benchmarks/bench_decode.py:33-97): the
+    default DecodeConfig (page 16, 32 q / 8 kv heads, head_dim 128, batch capacity 64),
+    split hints, the reference's input generator (seed 17, a pool of exactly the used
+    pages), one layer called eagerly -- plan build + attention + merge per call -- per
+    schedule, STATIC_CPU planning its lists on the host every call.  Alternating rounds of
+    `iterations` calls; GPU time per call from HIP events and host wall time per call,
+    medians.  Each schedule's output is checked against the FP32 oracle."""
+    import numpy as np
+    import torch
+    from oracle import attention as OA
+    from sglang_decode import workloads as W
+    from sglang_decode.config import DecodeConfig, Mode
+    from sglang_decode.planning.host_static import HostStatic
+    from sglang_decode.runtime.engine import DecodeEngine
+    lengths = REFERENCE_B
+    b = len(lengths)
+    per_workers, check = {}, {}
+    for workers in worker_counts:
+        c = DecodeConfig(workers=workers)
+        splits = W.split_hints(lengths, c.max_splits)
+        q, k, v, table = W.make_inputs(c, lengths, seed=17, device=dev, dtype=dtype)
+        if not check:
+            expected = OA.paged_attention_threads(q[:b].cpu(), k.cpu(), v.cpu(), table[:b].cpu(), lengths,
+                                                  c.page_size, threads=threads)[:b]
+        calls = {}
+        for name in ("R0", "R1", "STATIC", "STATIC_CPU", "D1", "D4"):
+            mode = Mode.R1 if name == "STATIC_CPU" else Mode[name]
+            eng = DecodeEngine(c, device=dev, dtype=dtype, force_mode=int(mode))
+            W.update_plan(eng, lengths, splits)
+            if name == "STATIC_CPU":
+                hs = HostStatic(eng)
+
+                def call(eng=eng, hs=hs):
+                    hs.plan_lists(lengths, splits)
+                    eng.prepare()
+                    hs.apply()
+                    return eng.execute(q, k, v, table)
+            else:
+                def call(eng=eng):
+                    eng.prepare()
+                    return eng.execute(q, k, v, table)
+            out = call()
+            torch.cuda.synchronize()
+            got = out[:b].float().cpu().numpy()
+            ok = bool(np.allclose(got, expected, atol=2e-2, rtol=1e-2))
+            prev = check.get(name)
+            check[name] = dict(ok=ok and (prev is None or prev["ok"]),
+                               max_abs_err=round(float(np.max(np.abs(got - expected))), 6))
+            for _ in range(max(1, iterations // 10)):
+                call()
+            calls[name] = call
+        torch.cuda.synchronize()
+        rows = {name: ([], []) for name in calls}
+        for trial in range(rounds):
+            for name in (list(calls) if trial % 2 == 0 else list(reversed(calls))):
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                wall0 = time.perf_counter_ns()
+                start.record()
+                for _ in range(iterations):
+                    calls[name]()
+                end.record()
+                end.synchronize()
+                rows[name][0].append(start.elapsed_time(end) * 1000.0 / iterations)
+                rows[name][1].append((time.perf_counter_ns() - wall0) / 1000.0 / iterations)
+        per_workers[str(workers)] = {name: dict(gpu_us=round(statistics.median(g), 2),
+                                                wall_us=round(statistics.median(w), 2)) for name, (g, w) in rows.items()}
+    dt = "bf16" if dtype == torch.bfloat16 else "fp16"
+    return dict(lengths="[256]*24 + [1536]*4 + [16384]*4",
+                config=f"DecodeConfig() defaults: batch capacity 64, 32q/8kv, D=128, page 16, max_splits 16, "
+                       f"split_hints; {dt}",
+                boundary="eager single-layer full entry (plan + attention + merge) per call",
+                iterations=iterations, rounds=rounds, workers=per_workers, check=check,
+                published=REFERENCE_B_PUBLISHED)
+
+
+def provenance(dev, args, config, lengths, splits):
+    """What produced this line: a hash of the sources that build and drive the path, the
+    software versions, the device, and a hash of the workload (benchmarks/common.py:12-30 of
+    the reference writes the same kind of manifest)."""
+    import hashlib
+    import platform
+    import subprocess
+    import torch
+    h = hashlib.sha256()
+    for base, exts in ((os.path.join(ROOT, "-sglang-decode-_amd"), (".hip", ".h", ".py")),
+                       (os.path.join(ROOT, "include"), (".h",))):
+        for dirpath, dirnames, files in sorted(os.walk(base)):
+            dirnames[:] = sorted(d for d in dirnames if not d.startswith(("_", ".")))
+            for f in sorted(files):
+                if f.endswith(exts):
+                    h.update(f.encode())
+                    with open(os.path.join(dirpath, f), "rb") as fh:
+                        h.update(fh.read())
+    with open(os.path.abspath(__file__), "rb") as fh:
+        h.update(fh.read())
+    try:
+        git = subprocess.run(["git", "rev-parse", "HEAD"], cwd=ROOT, capture_output=True, text=True,
+                             timeout=10).stdout.strip() or None
+    except (OSError, subprocess.SubprocessError):
+        git = None
+    props = torch.cuda.get_device_properties(dev)
+    wl = json.dumps(dict(config=repr(config), lengths=list(lengths), splits=list(splits)), sort_keys=True)
+    return dict(source_sha256=h.hexdigest()[:16], git=git, torch=torch.__version__, hip=torch.version.hip,
+                python=platform.python_version(), device=props.name,
+                arch=getattr(props, "gcnArchName", None), compute_units=props.multi_processor_count,
+                workload_sha256=hashlib.sha256(wl.encode()).hexdigest()[:16], argv=sys.argv[1:])
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -264,6 +388,9 @@ def main():
     workers = args.workers or default_workers(dev)
     dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
     c = W.config_for(args.workload, workers=workers)
+    if args.head_dim:
+        import dataclasses
+        c = dataclasses.replace(c, head_dim=args.head_dim)
     lengths = W.lengths_for(args.workload)
     splits = W.split_hints(lengths, c.max_splits)
     batch = len(lengths)
@@ -324,7 +451,10 @@ def main():
         mode = int(Mode.R1 if host_static else Mode[name])
         engine = DecodeEngine(c, device=dev, dtype=dtype, layers=layers, force_mode=mode, kernel=args.kernel)
         if host_static:
-            hs = hosts[name] = HostStatic(engine)
+            # the host lists go into the plan's static_head / static_next, which the R1 build
+            # inside the replay leaves alone; the replay then only forces STATIC
+            hs = HostStatic(engine)
+            hosts[name] = (hs, engine.prepare)
             t0 = time.perf_counter()
             hs.plan_lists(lengths, splits)
             torch.cuda.synchronize()
@@ -345,16 +475,22 @@ def main():
     torch.cuda.synchronize()
 
     # alternating rounds (benchmarks/bench_decode.py:76-91): the schedules in order on even
-    # rounds, reversed on odd ones; per round the mean of `steps` replays
+    # rounds, reversed on odd ones; per round the mean of `steps` replays.  STATIC_HOST plans
+    # its lists on the host and uploads them before every replay, as a decode step whose
+    # lengths change every step would (the reference's STATIC_CPU charges the host LPT on
+    # every call); wall_us therefore includes the host planning.
     rounds = {name: [] for name in engines}
     for trial in range(args.rounds):
         for name in (list(engines) if trial % 2 == 0 else list(reversed(engines))):
             graph = engines[name][1]
+            replan = hosts[name][0].plan_lists if name in hosts else None
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
             wall0 = time.perf_counter_ns()
             start.record()
             for _ in range(args.steps):
+                if replan is not None:
+                    replan(lengths, splits)
                 graph.replay()
             end.record()
             end.synchronize()
@@ -480,7 +616,7 @@ def main():
     # SGLang's two-stage split-KV decode on the same inputs and split counts, per layer over the
     # same rotating pools, captured in a HIP graph like the attention + merge figure
     upstream = None
-    if csr and not args.no_upstream and c.group_size <= 4:
+    if csr and not args.no_upstream and c.group_size <= 4 and c.head_dim == 128:
         from sglang_decode.kernels.upstream import decode_attention_fwd
         num = torch.tensor(splits, dtype=torch.int32, device=dev)
         up_logits = torch.empty((batch, c.query_heads, c.max_splits, c.head_dim), device=dev)
@@ -536,8 +672,11 @@ def main():
         calls = {}
         for name, (eng, gr) in engines.items():
             def call(name=name, eng=eng, gr=gr):
-                if name == "STATIC_HOST":
-                    hosts[name].prepare(lengths, splits)
+                if name == "STATIC_HOST":  # host LPT + upload, the R1 build, STATIC forced: once each
+                    hs, device_prepare = hosts[name]
+                    hs.plan_lists(lengths, splits)
+                    device_prepare()
+                    hs.apply()
                 else:
                     eng.prepare()
                 eng.execute(gr.q[0], *gr.kv_pairs[0], gr.pages[0], layer=0, indptr=gr.indptr[0])
@@ -561,6 +700,17 @@ def main():
         entry = {name: dict(gpu_us=round(statistics.median(g), 2), wall_us=round(statistics.median(w), 2))
                  for name, (g, w) in rows.items()}
         print(f"[bench] single-layer full entry per call (eager, reference boundary): {entry}", flush=True)
+
+    reference_b = None
+    if not args.no_reference_b and args.entry_iterations > 0:
+        cus = props.multi_processor_count
+        reference_b = time_reference_workload_b(dev, dtype, (cus, 2 * cus), args.entry_iterations, args.rounds,
+                                                cpu_threads)
+        print(f"[bench] reference workload B (eager full entry per call, us): {reference_b['workers']}; "
+              f"check {reference_b['check']}", flush=True)
+        if not all(v["ok"] for v in reference_b["check"].values()):
+            print("[bench] OUTPUT MISMATCH against the oracle on workload B", file=sys.stderr)
+            sys.exit(3)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -619,6 +769,8 @@ def main():
         "single_layer_entry_us": round(single_layer_us, 2),
         "entry": entry,
         "upstream_comparator": upstream,
+        "reference_workload_B": reference_b,
+        "provenance": provenance(dev, args, c, lengths, splits),
     }
     if kv_store is not None:
         line["kv_store"] = kv_store

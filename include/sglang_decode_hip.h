@@ -256,6 +256,20 @@ int sgd_host_static_lists(const int32_t *weight, int32_t record_count, int32_t k
                           int32_t *static_next);
 
 /*
+ * The same host lists from the step's plan inputs (lengths / splits [batch], host
+ * memory): the records of count_scan + emit_records (kernels/plan.py:7-45: chunk =
+ * ceil(ceil(L / S) / 32) * 32, weight = ceil(tokens / block_kv)) are formed in C++ and
+ * planned by the heap LPT above, as benchmarks/bench_decode.py:14-30 does per call through
+ * planning/reference.py:15-67.  Lengths outside [0, max_context], splits outside [1,
+ * max_splits] or more than task_capacity tasks are SGD_EINVAL.  *record_count (optional)
+ * receives the number of records.
+ */
+int sgd_host_static_plan(const int32_t *lengths, const int32_t *splits, int32_t batch, int32_t max_splits,
+                         int32_t max_context, int32_t block_kv, int32_t kv_heads, int32_t workers,
+                         int32_t task_capacity, int32_t *static_head, int32_t *static_next,
+                         int32_t *record_count);
+
+/*
  * Upstream SGLang's two-stage split-KV decode on gfx950: the comparator of the reference's
  * benchmark (benchmarks/baselines.py:8-34, over third_party/sglang/decode_attention.py:
  * 245-601 of SGLang v0.4.6.post5: decode_attention_fwd with its grouped stage 1 and its

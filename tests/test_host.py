@@ -181,6 +181,36 @@ def test_host_static_lists_cpp_matches_reference(plan_vectors):
         assert lib.sgd_host_static_lists(w, n, c.kv_heads, c.workers, cap, heads, nxt) == 0
         lists = R.lists_to_links(case["static_lists"], c.workers, cap)
         assert list(heads) == lists[0] and list(nxt) == lists[1], case["name"]
+        # the same lists from the plan inputs: records formed in C++ from lengths / splits
+        if not case.get("lengths"):
+            continue
+        b = len(case["lengths"])
+        ln = (ctypes.c_int32 * b)(*case["lengths"])
+        sp = (ctypes.c_int32 * b)(*case["splits"])
+        heads2, nxt2, count = (ctypes.c_int32 * c.workers)(), (ctypes.c_int32 * cap)(), ctypes.c_int32(-1)
+        assert lib.sgd_host_static_plan(ln, sp, b, c.max_splits, c.max_context, c.block_kv, c.kv_heads, c.workers,
+                                        cap, heads2, nxt2, ctypes.byref(count)) == 0, case["name"]
+        assert count.value == n, case["name"]
+        assert list(heads2) == lists[0] and list(nxt2) == lists[1], case["name"]
+
+
+def test_host_static_plan_rejects_bad_inputs():
+    """The C++ host planner refuses a length beyond max_context, a split count outside
+    [1, max_splits] and more tasks than the capacity, with the request named."""
+    from sglang_decode import _lib
+    lib = _lib.lib()
+    heads, nxt = (ctypes.c_int32 * 8)(), (ctypes.c_int32 * 64)()
+
+    def run(lengths, splits, max_context=1024, cap=64):
+        b = len(lengths)
+        return lib.sgd_host_static_plan((ctypes.c_int32 * b)(*lengths), (ctypes.c_int32 * b)(*splits), b, 4,
+                                        max_context, 128, 2, 8, cap, heads, nxt, None)
+
+    assert run([100, 1024], [1, 4]) == 0
+    assert run([100, 1025], [1, 4]) == -22 and b"request 1" in lib.sgd_last_error()
+    assert run([100, -1], [1, 1]) == -22
+    assert run([100], [0]) == -22 and run([100], [5]) == -22
+    assert run([1024] * 9, [4] * 9) == -22 and b"task capacity" in lib.sgd_last_error()  # 36 records x 2 > 64
 
 
 def test_abi_rejects_bad_arguments_before_launch():
@@ -254,6 +284,68 @@ def test_engine_validates_before_launch():
     assert engine.layers[0].partial.shape == (4, 8, 16, 128)
     assert engine.layers[0].lse.shape == (4, 8, 16)
     assert Mode.D4 == 4
+
+
+def test_noalloc_wrapper_validates_before_launch():
+    """decode_noalloc runs the engine's layout checks and sizes its plan inputs on the host:
+    a short lengths/splits tensor, an int64 page table, mixed q/K dtypes, a wrong q shape or
+    a mis-shaped out raise ValueError before the library is called (CPU tensors here)."""
+    import torch
+    from sglang_decode.kernels.noalloc import decode_noalloc
+    c = W.config_for("c1")
+    q = torch.zeros(c.batch_capacity, c.query_heads, c.head_dim, dtype=torch.bfloat16)
+    k = torch.zeros(64, c.kv_heads, c.head_dim, dtype=torch.bfloat16)
+    idx = torch.zeros(64, dtype=torch.int32)
+    indptr = torch.zeros(c.batch_capacity + 1, dtype=torch.int32)
+    lengths = torch.zeros(c.batch_capacity, dtype=torch.int32)
+    active = torch.ones(1, dtype=torch.int32)
+    out = torch.empty_like(q)
+
+    def call(**kw):
+        args = dict(q=q, k=k, v=k, pages=idx, lengths=lengths, splits=lengths.clone(), active=active, out=out,
+                    indptr=indptr)
+        args.update(kw)
+        ip = args.pop("indptr")
+        return decode_noalloc(c, **args, indptr=ip)
+
+    for kw, what in ((dict(lengths=lengths[:2]), "lengths"), (dict(splits=lengths[:3].clone()), "splits"),
+                     (dict(active=torch.ones(2, dtype=torch.int32)), "active"),
+                     (dict(lengths=lengths.long()), "lengths"), (dict(pages=idx.long()), "int32"),
+                     (dict(k=k.half(), v=k.half()), "dtype"), (dict(q=q[:2], out=out[:2]), "q must be"),
+                     (dict(out=out[:, :, :64]), "out must be"), (dict(out=out.float()), "output"),
+                     (dict(k=k[:, :1], v=k[:, :1]), "CSR K and V"),
+                     (dict(indptr=indptr.long()), "kv_indptr")):
+        with pytest.raises(ValueError, match=what):
+            call(**kw)
+
+
+def test_upstream_wrapper_validates_before_launch():
+    """decode_attention_fwd checks the metadata sizes its stages index (kv_indptr[b + 1],
+    num_kv_splits[b] for b < batch), K/V shape and dtype, and one device."""
+    import torch
+    from sglang_decode.kernels.upstream import decode_attention_fwd
+    b, hq, hkv, d, s = 3, 8, 2, 128, 4
+    q = torch.zeros(b, hq, d, dtype=torch.bfloat16)
+    k = torch.zeros(32, hkv, d, dtype=torch.bfloat16)
+    o = torch.empty_like(q)
+    indptr = torch.zeros(b + 1, dtype=torch.int32)
+    idx = torch.zeros(32, dtype=torch.int32)
+    num = torch.ones(b, dtype=torch.int32)
+    logits = torch.empty(b, hq, s, d)
+    lse = torch.empty(b, hq, s)
+
+    def call(**kw):
+        args = dict(q=q, k_buffer=k, v_buffer=k, o=o, kv_indptr=indptr, kv_indices=idx, attn_logits=logits,
+                    attn_lse=lse, num_kv_splits=num, max_kv_splits=s, sm_scale=0.1)
+        args.update(kw)
+        return decode_attention_fwd(**args)
+
+    for kw, what in ((dict(kv_indptr=indptr[:b]), "kv_indptr"), (dict(num_kv_splits=num[:b - 1]), "num_kv_splits"),
+                     (dict(k_buffer=k.half(), v_buffer=k.half()), "dtype"), (dict(k_buffer=k[0], v_buffer=k[0]),
+                                                                              "k_buffer"),
+                     (dict(v_buffer=k[:16]), "k_buffer"), (dict(kv_indptr=indptr.long()), "kv_indptr")):
+        with pytest.raises(ValueError, match=what):
+            call(**kw)
 
 
 def test_host_static_schedule_installs_reference_lists(plan_vectors):
