@@ -18,13 +18,19 @@ constexpr float kLn2 = 0.6931471805599453f;
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-// One wave's staging area: the K and V rows of a 16-token tile (row-major, 256 B
-// rows) and the tile's probabilities as token pairs.
+// One wave's staging area: the K and V rows of a 16-token tile (256 B rows) and the
+// tile's probabilities as token pairs.  K rows of odd tokens hold their two 128 B
+// halves swapped (16 B chunk c at c ^ 8, k_chunk): the QK reads take 8 lanes per
+// token row, and the 16 lanes the LDS serves per cycle then cover all 64 banks
+// instead of the same 32 twice.  V rows are plain: their reads cover 256 B per 32 lanes.
 struct WaveTile {
     uint4 k[kTile][kD / 8];          // 4 KB
     uint4 v[kTile][kD / 8];          // 4 KB
     uint4 p[kTile / 2];              // [pair] -> 4 heads x (p[2i], p[2i+1]) in the KV dtype
 };
+
+// Position of 16 B chunk c of K row `row` in WaveTile::k.
+__device__ __forceinline__ constexpr int k_chunk(int row, int c) { return c ^ ((row & 1) << 3); }
 
 template <int DT>
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -156,7 +162,7 @@ __device__ __forceinline__ void tile_stage(WaveTile &wt, uint4 (&kr)[kRowsLoads]
     }
 #pragma unroll
     for (int i = 0; i < kRowsLoads; ++i) {
-        wt.k[4 * i + (lane >> 4)][lane & 15] = kr[i];
+        wt.k[4 * i + (lane >> 4)][k_chunk(lane >> 4, lane & 15)] = kr[i];
         wt.v[4 * i + (lane >> 4)][lane & 15] = vr[i];
     }
 }
@@ -172,7 +178,7 @@ __device__ __forceinline__ void tile_compute(WaveTile &wt, const uint4 (*qs)[kD 
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
         const int tk = 8 * pass + ro.qg;
-        const uint4 lo = wt.k[tk][ro.qj], hi = wt.k[tk][ro.qj + 8];
+        const uint4 lo = wt.k[tk][k_chunk(tk, ro.qj)], hi = wt.k[tk][k_chunk(tk, ro.qj + 8)];
         const uint32_t kv[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         float sh4[kHeads];
 #pragma unroll
