@@ -12,7 +12,9 @@ is None and ``make_backend_class(base)`` builds the same subclass over any base
 class that provides the upstream attributes (used by the host-side tests).
 
 Environment: DECODE_DISABLE=1 keeps upstream decode; DECODE_MODE=AUTO|R0|R1|
-STATIC|D1|D4 forces a schedule; DECODE_POLICY=<validated policy json>;
+STATIC|D1|D4 forces a schedule; DECODE_POLICY=<validated policy json> picks the
+schedule per batch shape (unset: the artifact shipped for the GPU's architecture,
+policies/mi355x.json on gfx950; "none": no rules, R1 as in the reference);
 DECODE_BATCH_CAPACITY (default 64); DECODE_REUSE_PLAN=0 rebuilds the plan on
 every layer; DECODE_WORKERS overrides the persistent worker count (default: two
 per compute unit); DECODE_FUSED_KV=0 keeps upstream's set_kv_buffer and a separate
@@ -27,7 +29,7 @@ import torch
 
 from ..config import WORKGROUPS_PER_CU, DecodeConfig, Mode
 from ..kernels.kv_store import store_kv_and_stage_q
-from ..planning.policy import load_policy
+from ..planning.policy import policy_from_env
 
 try:  # pragma: no cover - depends on an optional install
     from sglang.srt.layers.attention.triton_backend import TritonAttnBackend as _UpstreamBackend
@@ -96,7 +98,7 @@ def make_backend_class(base):
                 page_size=1, workers=workers)
             mode_name = os.getenv("DECODE_MODE", "AUTO")
             force = -1 if mode_name == "AUTO" else int(Mode[mode_name])
-            rules = load_policy(os.getenv("DECODE_POLICY"))
+            rules = policy_from_env(self.device)
             # Indexed by absolute layer_id.
             layers = model_runner.model_config.hf_config.num_hidden_layers
             self.scheduled = DecodeEngine(config, self.device, dtype, layers, rules, force)

@@ -19,9 +19,14 @@ and messages are this package's:
 * The artifact -- ``{"status": "validated", "evidence": [{path, sha256}, ...], "rules":
   [{min_tasks, max_tasks, min_ratio, max_ratio, mode}]}`` -- is written only to a path
   that does not exist yet, and ``planning.policy.load_policy`` reads it.
+* Several shapes may share one artifact: each ``--rule`` names its own calibration and
+  holdout files and the task / weight-ratio ranges its rule covers, every one passes the
+  gate on its own files, and the artifact is written only when all of them pass (rules in
+  the order given; the device plan lets the last matching rule win).
 
 Usage: ``python -m sglang_decode.planning.calibrate CAL.csv HOLDOUT.csv --output
-policy.json --tasks MIN MAX --ratio MIN MAX``.
+policy.json --tasks MIN MAX --ratio MIN MAX``, or ``... --output policy.json --rule CAL.csv
+HOLDOUT.csv TASKS_MIN TASKS_MAX RATIO_MIN RATIO_MAX [--rule ...]``.
 """
 import argparse
 import csv
@@ -95,17 +100,34 @@ def choose(calibration: Samples, holdout: Samples):
 
 
 def calibrate(calibration_path, holdout_path, output, tasks, ratio):
-    """Writes the validated artifact to ``output`` (which must not exist) and returns it."""
-    cal_path, hold_path, output = Path(calibration_path), Path(holdout_path), Path(output)
-    if cal_path.resolve() == hold_path.resolve():
-        raise ValueError("the holdout set must be an independent file, not the calibration set")
-    pick = choose(Samples(cal_path), Samples(hold_path))
-    rule = dict(min_tasks=int(tasks[0]), max_tasks=int(tasks[1]), min_ratio=int(ratio[0]),
-                max_ratio=int(ratio[1]), mode=int(SCHEDULES[pick]))
+    """Writes the validated one-rule artifact to ``output`` (which must not exist) and
+    returns it."""
+    return calibrate_rules([(calibration_path, holdout_path, tasks, ratio)], output)
+
+
+def calibrate_rules(groups, output):
+    """``groups``: (calibration path, holdout path, (min_tasks, max_tasks), (min_ratio,
+    max_ratio)) per rule.  Every group must pass the gate; then the artifact with one rule
+    per group (in order) is written to ``output`` (which must not exist) and returned."""
+    output = Path(output)
+    if not groups:
+        raise ValueError("no rule to calibrate")
+    rules, files = [], []
+    for cal, hold, tasks, ratio in groups:
+        cal_path, hold_path = Path(cal), Path(hold)
+        if cal_path.resolve() == hold_path.resolve():
+            raise ValueError("the holdout set must be an independent file, not the calibration set")
+        if not (0 <= int(tasks[0]) <= int(tasks[1]) and 100 <= int(ratio[0]) <= int(ratio[1])):
+            raise ValueError(f"rule ranges tasks {tuple(tasks)} / ratio {tuple(ratio)}: need 0 <= min <= max "
+                             "and a weight ratio of at least 100")
+        pick = choose(Samples(cal_path), Samples(hold_path))
+        rules.append(dict(min_tasks=int(tasks[0]), max_tasks=int(tasks[1]), min_ratio=int(ratio[0]),
+                          max_ratio=int(ratio[1]), mode=int(SCHEDULES[pick])))
+        files += [cal_path, hold_path]
     artifact = dict(status="validated",
                     evidence=[dict(path=str(p), sha256=hashlib.sha256(p.read_bytes()).hexdigest())
-                              for p in (cal_path, hold_path)],
-                    rules=[rule])
+                              for p in files],
+                    rules=rules)
     with output.open("x") as f:  # never replace an existing artifact
         json.dump(artifact, f, indent=2)
     return artifact
@@ -113,14 +135,23 @@ def calibrate(calibration_path, holdout_path, output, tasks, ratio):
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
-    ap.add_argument("calibration", type=Path)
-    ap.add_argument("holdout", type=Path)
+    ap.add_argument("calibration", type=Path, nargs="?")
+    ap.add_argument("holdout", type=Path, nargs="?")
     ap.add_argument("--output", type=Path, required=True)
-    ap.add_argument("--tasks", nargs=2, type=int, required=True, metavar=("MIN", "MAX"))
-    ap.add_argument("--ratio", nargs=2, type=int, required=True, metavar=("MIN", "MAX"))
+    ap.add_argument("--tasks", nargs=2, type=int, metavar=("MIN", "MAX"))
+    ap.add_argument("--ratio", nargs=2, type=int, metavar=("MIN", "MAX"))
+    ap.add_argument("--rule", nargs=6, action="append", default=[],
+                    metavar=("CAL", "HOLDOUT", "TASKS_MIN", "TASKS_MAX", "RATIO_MIN", "RATIO_MAX"))
     args = ap.parse_args(argv)
+    single = (args.calibration, args.holdout, args.tasks, args.ratio)
+    if args.rule and any(x is not None for x in single):
+        ap.error("give either CAL HOLDOUT --tasks --ratio or --rule groups, not both")
+    if not args.rule and any(x is None for x in single):
+        ap.error("CAL, HOLDOUT, --tasks and --ratio are required without --rule")
+    groups = [(args.calibration, args.holdout, args.tasks, args.ratio)] if not args.rule else [
+        (Path(r[0]), Path(r[1]), (int(r[2]), int(r[3])), (int(r[4]), int(r[5]))) for r in args.rule]
     try:
-        calibrate(args.calibration, args.holdout, args.output, args.tasks, args.ratio)
+        calibrate_rules(groups, args.output)
     except ValueError as e:
         ap.error(str(e))
     except GateRejected as e:

@@ -15,7 +15,7 @@ splits), `--workload c4` the Llama-3-70B paged layer (page 16, 64 q / 8 kv, batc
 c5` the 32-layer step of the 8B shape at batch 64 (contexts lognormal, median 2048)
 with a 256k-token pool per layer.
 
-Reported per schedule (R1, STATIC, STATIC_HOST, D1, D4, R0), timed in 5 alternating
+Reported per schedule (R1, STATIC, STATIC_HOST, D1, D4, R0, AUTO), timed in 5 alternating
 rounds as the reference's benchmark does (benchmarks/bench_decode.py:76-91): us/layer =
 replay time / layers, achieved GB/s = algorithmic bytes per layer / us/layer, and an
 oracle check (layer 0 within 2e-2 abs / 1e-2 rel of the FP32 oracle, and every layer that
@@ -23,7 +23,10 @@ reads the same pool bitwise equal to it).  STATIC builds its LPT lists on the de
 inside the replay (the reference's device greedy, a serial chain); STATIC_HOST is the
 reference benchmark's host-static variant (benchmarks/bench_decode.py:14-30): C++ heap
 LPT on the host when the lengths change, uploaded from pinned memory, installed after
-the device R1 plan.  `value` is the achieved HBM GB/s of the fastest schedule.
+the device R1 plan.  AUTO is the adapter's default: no forced mode, the policy artifact
+shipped for this GPU (planning.policy.shipped_policy; R1 where none ships) choosing on the
+device plan; `default_schedule` names the artifact and the mode its rules picked.
+`value` is the achieved HBM GB/s of the fastest schedule.
 `roofline` times the attention kernel alone for that schedule: a HIP graph of
 back-to-back launches (rotating layers) replayed between HIP events on its stream.
 `attention_merge_us` (attention + merge per layer, no plan) and `single_layer_entry_us`
@@ -49,7 +52,7 @@ for _p in (os.path.join(ROOT, "-sglang-decode-_amd"), ROOT):
 
 METRIC = "decode-attn µs/layer + achieved HBM GB/s (% peak), Llama-3-8B GQA shape B=64"
 PEAK_HBM_GBS = 8000.0
-POLICIES = ("R1", "STATIC", "STATIC_HOST", "D1", "D4", "R0")
+POLICIES = ("R1", "STATIC", "STATIC_HOST", "D1", "D4", "R0", "AUTO")
 WORKLOADS = {
     "c2": "llama3-8b decode layer: B=64, 32q/8kv, D=128, bf16, CSR page 1, lognormal(median 1024) "
           "contexts clipped [128,8192], 1M-token pool per layer",
@@ -381,6 +384,7 @@ def main():
     from sglang_decode.runtime.engine import DecodeEngine, PlanKey
     from sglang_decode.runtime.graph import DecodeGraph
     from sglang_decode.planning.host_static import HostStatic
+    from sglang_decode.planning.policy import load_policy, shipped_policy
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
@@ -446,10 +450,13 @@ def main():
 
     engines, hosts, samples = {}, {}, []
     host_lpt_us = None
+    auto_policy = shipped_policy(dev)
     for name in [p for p in args.policies.split(",") if p]:
         host_static = name == "STATIC_HOST"
-        mode = int(Mode.R1 if host_static else Mode[name])
-        engine = DecodeEngine(c, device=dev, dtype=dtype, layers=layers, force_mode=mode, kernel=args.kernel)
+        auto = name == "AUTO"
+        mode = -1 if auto else int(Mode.R1 if host_static else Mode[name])
+        engine = DecodeEngine(c, device=dev, dtype=dtype, layers=layers, force_mode=mode, kernel=args.kernel,
+                              rules=load_policy(auto_policy) if auto else ())
         if host_static:
             # the host lists go into the plan's static_head / static_next, which the R1 build
             # inside the replay leaves alone; the replay then only forces STATIC
@@ -508,6 +515,13 @@ def main():
                              gbps=bytes_per_layer / (us_layer * 1e-6) / 1e9)
         print(f"[bench] {name}: {us_layer:.2f} us/layer  {results[name]['gbps']:.0f} GB/s "
               f"({100 * results[name]['gbps'] / PEAK_HBM_GBS:.1f}% of peak)", flush=True)
+
+    default_schedule = None
+    if "AUTO" in engines:  # the mode the shipped policy's rules picked on the device plan
+        picked = Mode(int(engines["AUTO"][0].plan.mode.item())).name
+        default_schedule = dict(policy=os.path.relpath(auto_policy, ROOT) if auto_policy else None, mode=picked,
+                                us_per_layer=round(results["AUTO"]["us_per_layer"], 2))
+        print(f"[bench] AUTO (adapter default): policy {default_schedule['policy']} picked {picked}", flush=True)
 
     if args.samples_csv:
         import csv
@@ -762,6 +776,7 @@ def main():
         "kv_tokens_per_s": round(sum(lengths) / (r["us_per_layer"] * 1e-6), 1),
         "schedules": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in results.items()},
         "host_lpt_us": None if host_lpt_us is None else round(host_lpt_us, 1),
+        "default_schedule": default_schedule,
         "check": check,
         "roofline": roofline,
         "cpu_baseline": cpu,
