@@ -1,8 +1,8 @@
 // Persistent paged GQA decode attention for query-head groups of up to 4 heads
-// (Llama-3-8B: 32 q / 8 kv), head_dim 128, unit dim stride -- the per-task VALU
-// kernel.
+// (Llama-3-8B: 32 q / 8 kv), head_dim 64, 128 or 256, unit dim stride -- the
+// per-task VALU kernel.
 //
-// Contraction sizes per token are 4 heads x 128 dims for QK^T and for P.V: far
+// Contraction sizes per token are 4 heads x D dims for QK^T and for P.V: far
 // too narrow for a dense MFMA tile, so the math runs on the VALU with packed
 // 16-bit dot products (v_dot2_f32_bf16 / _f16, fp32 accumulate) and wave64 DPP
 // reductions (valu_ops.h).  The kernel is HBM-bound.
@@ -11,8 +11,9 @@
 // 16 waves per CU in both cases -- the load concurrency the random 256 B row
 // gathers need, and enough waves to hide the tile math (~395 VALU instructions per
 // tile and wave, about 40% of the SIMDs' issue slots over a launch).  Tasks come from the plan's dispatch (attention_common.h); each
-// task (record, kv head) is dealt to the waves in 16-token tiles (tile i -> wave
-// i % kWaves).  Per wave and tile: gather K and V rows (4 x 16 B loads each), stage
+// task (record, kv head) is dealt to the waves in tiles of 2048 / D tokens (4 KB of K
+// and of V; tile i -> wave i % kWaves).  Per wave and tile: gather K and V rows (4 x 16
+// B loads each), stage
 // them in the wave's LDS tile shared by the group's query heads, QK^T with a DPP
 // reduce-scatter, online softmax in the exp2 domain, P rounded to the KV dtype
 // (kernels/attention.py:78), P.V over token pairs.  The next tile's K/V loads and
@@ -32,10 +33,11 @@ using namespace valu;
 
 constexpr int kIndptrLds = 256;  // CSR: kv_indptr entries kept in LDS (rows beyond read memory)
 
-template <int kWaves>
+template <int kWaves, int D>
 struct ValuShared {
-    WaveTile w[kWaves];
-    uint4 q[kHeads][kD / 8];         // q rows of the current task
+    static constexpr int kTile = Geo<D>::kTile;
+    WaveTile<D> w[kWaves];
+    uint4 q[kHeads][D / 8];          // q rows of the current task
     float cm[kWaves][kHeads];
     float cd[kWaves][kHeads];
     int32_t indptr[kIndptrLds];
@@ -45,15 +47,17 @@ struct ValuShared {
 };
 
 // ------------------------------------------------------------------ kernel
-template <int DT, bool CSR, int kWaves>
+template <int DT, bool CSR, int kWaves, int D>
 __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_args a) {
     // 16 waves per CU (two 8-wave or one 16-wave workgroup): the load concurrency the
     // random row gathers need to approach the HBM ceiling (4 waves per SIMD, <= 128
     // VGPRs).
     extern __shared__ __align__(16) char dyn_smem[];
-    ValuShared<kWaves> &sh = *reinterpret_cast<ValuShared<kWaves> *>(dyn_smem);
+    using Sh = ValuShared<kWaves, D>;
+    constexpr int kTile = Geo<D>::kTile, kQChunks = kHeads * D / 8, kQPerLane = (kQChunks + 63) / 64;
+    Sh &sh = *reinterpret_cast<Sh *>(dyn_smem);
     const int lane0 = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
-    WaveTile &wt = sh.w[wave];
+    WaveTile<D> &wt = sh.w[wave];
     const int32_t G = a.query_heads / a.kv_heads;
     const float scale2 = a.scale * kLog2e;
     const int page_shift = __builtin_ctz((unsigned)a.page_size);  // page_size is a power of two here
@@ -74,17 +78,20 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
         // Global loads first -- q rows (wave 0), then the request's index base, the first
         // tile's indices and its K/V rows into registers -- so that they are in flight
         // across the barriers that hand shared memory over from the previous task.
-        uint4 qrow = make_uint4(0, 0, 0, 0);  // wave 0: head lane / 16, dims 8 (lane % 16) ..; zero past G
-        if (wave == 0) {
-            const int h = lane >> 4, c = lane & 15;
-            if (h < G) {
+        // wave 0: 16 B chunk lane + 64 j of the group's q rows (head = chunk / (D / 8)); zero past G
+        uint4 qrow[kQPerLane];
+#pragma unroll
+        for (int j = 0; j < kQPerLane; ++j) {
+            qrow[j] = make_uint4(0, 0, 0, 0);
+            const int ci = lane + 64 * j, h = ci / (D / 8), c = ci % (D / 8);
+            if (wave == 0 && ci < kQChunks && h < G) {
                 const int32_t qd = (int32_t)a.q_stride[2];
                 const uint16_t *qp = static_cast<const uint16_t *>(a.q) + (int64_t)ti.request * a.q_stride[0] +
                                      (int64_t)(ti.group * G + h) * a.q_stride[1] + (int64_t)(c * 8) * qd;
                 uint32_t w4[4] = {0, 0, 0, 0};
 #pragma unroll
                 for (int e = 0; e < 8; ++e) w4[e >> 1] |= (uint32_t)qp[e * qd] << (16 * (e & 1));
-                qrow = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+                qrow[j] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
             }
         }
         TileSrc T;
@@ -107,16 +114,22 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
         if (n0 > 0) {
             int32_t i0;
             if (prefetched) {
-                const int i = lane & 15;
-                i0 = i < kRowsLoads ? sh.pf_idx[succ.cur][wave * kTile + 4 * i + (lane >> 4)] : 0;
+                const int row = index_row<D>(lane);
+                i0 = row >= 0 ? sh.pf_idx[succ.cur][wave * kTile + row] : 0;
             } else {
-                i0 = tile_index<CSR>(a, T, T.start + wave * kTile, lane, page_shift);
+                i0 = tile_index<CSR, D>(a, T, T.start + wave * kTile, lane, page_shift);
             }
-            tile_issue<CSR>(T, wave, i0, page_mask, lane, kr, vr);
-            if (n0 > 1) idx_next = tile_index<CSR>(a, T, T.start + (wave + kWaves) * kTile, lane, page_shift);
+            tile_issue<CSR, D>(T, wave, i0, page_mask, lane, kr, vr);
+            if (n0 > 1) idx_next = tile_index<CSR, D>(a, T, T.start + (wave + kWaves) * kTile, lane, page_shift);
         }
         lds_barrier();  // the previous task's merge is done with shared memory
-        if (wave == 0) sh.q[lane >> 4][lane & 15] = qrow;
+        if (wave == 0) {
+#pragma unroll
+            for (int j = 0; j < kQPerLane; ++j) {
+                const int ci = lane + 64 * j;
+                if (ci < kQChunks) sh.q[ci / (D / 8)][ci % (D / 8)] = qrow[j];
+            }
+        }
         lds_barrier();
         float m_l = -INFINITY, den_l = 0.f;  // this lane's head (QK roles)
         float acc[kHeads][4];
@@ -130,14 +143,15 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
             // per-lane LDS addresses each tile instead of holding them all live.
             int lane_v = lane;
             asm volatile("" : "+v"(lane_v));
-            const Roles ro(lane_v);
+            const Roles<D> ro(lane_v);
             const int32_t tile = wave + kWaves * e;
             const int32_t nvalid = min(kTile, T.end - (T.start + tile * kTile));
-            tile_stage(wt, kr, vr, lane_v, nvalid);
-            if (e + 1 < n0) tile_issue<CSR>(T, tile + kWaves, idx_next, page_mask, lane, kr, vr);
-            if (e + 2 < n0) idx_next = tile_index<CSR>(a, T, T.start + (tile + 2 * kWaves) * kTile, lane, page_shift);
+            tile_stage<D>(wt, kr, vr, lane_v, nvalid);
+            if (e + 1 < n0) tile_issue<CSR, D>(T, tile + kWaves, idx_next, page_mask, lane, kr, vr);
+            if (e + 2 < n0)
+                idx_next = tile_index<CSR, D>(a, T, T.start + (tile + 2 * kWaves) * kTile, lane, page_shift);
             wave_sync();
-            tile_compute<DT>(wt, sh.q, nvalid, scale2, ro, m_l, den_l, acc);
+            tile_compute<DT, D>(wt, sh.q, nvalid, scale2, ro, m_l, den_l, acc);
         }
 
         // ---- end of the wave's tiles.  The last wave has the fewest tiles (round-robin
@@ -147,14 +161,15 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
         if (wave == kWaves - 1)
             prefetch_next<CSR, kTile * kWaves>(a, succ, sh.pf_idx, lane, page_shift, sh.indptr, iptr_n);
         // ---- reduce within the wave, then merge the waves
-        const Roles ro(lane);
+        const Roles<D> ro(lane);
         float mh[kHeads], dh[kHeads];
-        wave_state(m_l, den_l, acc, mh, dh);
-        float *comb = reinterpret_cast<float *>(&wt.k[0][0]);  // [head][128] fp32, reuses this wave's K tile
-        if (lane < 32) {
+        wave_state<D>(m_l, den_l, acc, mh, dh);
+        float *comb = reinterpret_cast<float *>(&wt.k[0][0]);  // [head][D] fp32, reuses this wave's K tile
+        static_assert(sizeof(float) * kHeads * D <= sizeof(wt.k), "the combine rows fit the K tile");
+        if (lane < Geo<D>::kPvLanes) {
 #pragma unroll
             for (int h = 0; h < kHeads; ++h)
-                *reinterpret_cast<float4 *>(&comb[h * kD + ro.pd * 4]) =
+                *reinterpret_cast<float4 *>(&comb[h * D + ro.pd * 4]) =
                     make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
         }
         float mv = mh[0], dv = dh[0];
@@ -169,9 +184,10 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
             sh.cd[wave][lane] = dv;
         }
         lds_barrier();
-        if (threadIdx.x < kHeads * kD) {  // one (head, dim) output per thread: 4 heads x 128 dims
-            static_assert(kWaves * 64 >= kHeads * kD, "merge maps one thread per output");
-            const int h = threadIdx.x / kD, d = threadIdx.x % kD;
+        // one (head, dim) output per thread and round: 4 heads x D dims
+#pragma unroll
+        for (int o = threadIdx.x; o < kHeads * D; o += 64 * kWaves) {
+            const int h = o / D, d = o % D;
             if (h < G) {
                 float mm = -INFINITY;
 #pragma unroll
@@ -181,32 +197,32 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
                 for (int w = 0; w < kWaves; ++w) {
                     const float sc = __builtin_amdgcn_exp2f(sh.cm[w][h] - mm);
                     dd += sh.cd[w][h] * sc;
-                    x += reinterpret_cast<const float *>(&sh.w[w].k[0][0])[h * kD + d] * sc;
+                    x += reinterpret_cast<const float *>(&sh.w[w].k[0][0])[h * D + d] * sc;
                 }
                 const int64_t slot = ((int64_t)T.request * a.query_heads + group * G + h) * a.max_splits + split;
-                a.partial[slot * kD + d] = x / dd;
+                a.partial[slot * D + d] = x / dd;
                 if (d == 0) a.lse[slot] = (mm + __log2f(dd)) * kLn2;
             }
         }
     }, sh.pf);
 }
 
-template <int DT, bool CSR, int kWaves>
+template <int DT, bool CSR, int kWaves, int D>
 int launch_valu_w(const sgd_decode_args &a, hipStream_t stream) {
     static bool attr = false;
-    const int bytes = (int)sizeof(ValuShared<kWaves>);
+    const int bytes = (int)sizeof(ValuShared<kWaves, D>);
     if (!attr) {
-        if (hipFuncSetAttribute((const void *)k_attention_valu<DT, CSR, kWaves>,
+        if (hipFuncSetAttribute((const void *)k_attention_valu<DT, CSR, kWaves, D>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
             return einval("valu attention: cannot reserve %d B of LDS", bytes);
         attr = true;
     }
-    hipLaunchKernelGGL((k_attention_valu<DT, CSR, kWaves>), dim3(a.workers), dim3(64 * kWaves), bytes, stream, a);
+    hipLaunchKernelGGL((k_attention_valu<DT, CSR, kWaves, D>), dim3(a.workers), dim3(64 * kWaves), bytes, stream, a);
     return launch_status("persistent_decode(valu)");
 }
 
 // Waves per workgroup from the environment variable SGD_VALU_WAVES (8 or 16, default 8:
-// two workgroups per CU, the default worker count).
+// two workgroups per CU, the default worker count; 16 is built for head_dim 128 only).
 int valu_waves() {
     static int w = [] {
         const char *e = getenv("SGD_VALU_WAVES");
@@ -217,14 +233,20 @@ int valu_waves() {
 
 template <int DT, bool CSR>
 int launch_valu_t(const sgd_decode_args &a, hipStream_t stream) {
-    return valu_waves() == 8 ? launch_valu_w<DT, CSR, 8>(a, stream) : launch_valu_w<DT, CSR, 16>(a, stream);
+    switch (a.head_dim) {
+        case 64: return launch_valu_w<DT, CSR, 8, 64>(a, stream);
+        case 256: return launch_valu_w<DT, CSR, 8, 256>(a, stream);
+        default:
+            return valu_waves() == 8 ? launch_valu_w<DT, CSR, 8, 128>(a, stream)
+                                     : launch_valu_w<DT, CSR, 16, 128>(a, stream);
+    }
 }
 
 }  // namespace
 
 bool valu_supported(const sgd_decode_args &a) {
     const int g = a.query_heads / a.kv_heads;
-    if (g > kHeads || a.head_dim != kD) return false;
+    if (g > kHeads || (a.head_dim != 64 && a.head_dim != 128 && a.head_dim != 256)) return false;
     if (a.k_stride[3] != 1 || a.v_stride[3] != 1) return false;
     if ((reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.v)) & 15) return false;
     if (a.page_size & (a.page_size - 1)) return false;

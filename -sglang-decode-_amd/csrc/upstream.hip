@@ -22,9 +22,11 @@ namespace {
 using namespace valu;
 
 constexpr int kUpWaves = 8;
+constexpr int kD = 128;  // upstream's comparator runs the 8B head shape only
+constexpr int kTile = Geo<kD>::kTile;
 
 struct UpShared {
-    WaveTile w[kUpWaves];
+    WaveTile<kD> w[kUpWaves];
     uint4 q[kHeads][kD / 8];
     float cm[kUpWaves][kHeads];
     float cd[kUpWaves][kHeads];
@@ -50,7 +52,7 @@ __global__ __launch_bounds__(64 * kUpWaves, 4) void k_upstream_split(sgd_decode_
     const int2 range = split_range(a.indptr, num_splits, b, split, a.max_splits, chunk, length);
     if (range.y <= range.x) return;  // uniform over the workgroup
     const int lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
-    WaveTile &wt = sh.w[wave];
+    WaveTile<kD> &wt = sh.w[wave];
     const int32_t G = a.query_heads / a.kv_heads;
     const float scale2 = a.scale * kLog2e;
 
@@ -70,9 +72,9 @@ __global__ __launch_bounds__(64 * kUpWaves, 4) void k_upstream_split(sgd_decode_
     uint4 kr[kRowsLoads], vr[kRowsLoads];
     int32_t idx_next = 0;
     if (n0 > 0) {
-        const int32_t i0 = tile_index<true>(a, T, T.start + wave * kTile, lane, 0);
-        tile_issue<true>(T, wave, i0, 0, lane, kr, vr);
-        if (n0 > 1) idx_next = tile_index<true>(a, T, T.start + (wave + kUpWaves) * kTile, lane, 0);
+        const int32_t i0 = tile_index<true, kD>(a, T, T.start + wave * kTile, lane, 0);
+        tile_issue<true, kD>(T, wave, i0, 0, lane, kr, vr);
+        if (n0 > 1) idx_next = tile_index<true, kD>(a, T, T.start + (wave + kUpWaves) * kTile, lane, 0);
     }
     if (wave == 0) {  // q rows of the group: head lane / 16, dims 8 (lane % 16) ..; zero past G
         const int h = lane >> 4, c = lane & 15;
@@ -96,19 +98,19 @@ __global__ __launch_bounds__(64 * kUpWaves, 4) void k_upstream_split(sgd_decode_
 #pragma unroll
         for (int d = 0; d < 4; ++d) acc[h][d] = 0.f;
     for (int32_t e = 0; e < n0; ++e) {
-        const Roles ro(lane);
+        const Roles<kD> ro(lane);
         const int32_t tile = wave + kUpWaves * e;
         const int32_t nvalid = min(kTile, T.end - (T.start + tile * kTile));
-        tile_stage(wt, kr, vr, lane, nvalid);
-        if (e + 1 < n0) tile_issue<true>(T, tile + kUpWaves, idx_next, 0, lane, kr, vr);
-        if (e + 2 < n0) idx_next = tile_index<true>(a, T, T.start + (tile + 2 * kUpWaves) * kTile, lane, 0);
+        tile_stage<kD>(wt, kr, vr, lane, nvalid);
+        if (e + 1 < n0) tile_issue<true, kD>(T, tile + kUpWaves, idx_next, 0, lane, kr, vr);
+        if (e + 2 < n0) idx_next = tile_index<true, kD>(a, T, T.start + (tile + 2 * kUpWaves) * kTile, lane, 0);
         wave_sync();
-        tile_compute<DT>(wt, sh.q, nvalid, scale2, ro, m_l, den_l, acc);
+        tile_compute<DT, kD>(wt, sh.q, nvalid, scale2, ro, m_l, den_l, acc);
     }
     // the waves' states: per-head (m, den) to LDS, acc into the wave's K tile area
-    const Roles ro(lane);
+    const Roles<kD> ro(lane);
     float mh[kHeads], dh[kHeads];
-    wave_state(m_l, den_l, acc, mh, dh);
+    wave_state<kD>(m_l, den_l, acc, mh, dh);
     float *comb = reinterpret_cast<float *>(&wt.k[0][0]);
     if (lane < 32) {
 #pragma unroll
@@ -202,7 +204,7 @@ extern "C" int sgd_upstream_decode(const void *q, const void *k, const void *v, 
         kv_heads > 65535)
         return einval("upstream_decode: heads %d/%d (the tile math takes groups of up to %d)", query_heads, kv_heads,
                       valu::kHeads);
-    if (head_dim != valu::kD) return einval("upstream_decode: head_dim %d (128 only)", head_dim);
+    if (head_dim != kD) return einval("upstream_decode: head_dim %d (128 only)", head_dim);
     if (dtype != SGD_BF16 && dtype != SGD_FP16) return einval("upstream_decode: dtype %d", dtype);
     for (int i = 0; i < 4; ++i)
         if (kv_strides[i] % 8 || kv_strides[i] <= 0 || kv_strides[i] >= (1ll << 40))

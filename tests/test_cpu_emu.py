@@ -61,6 +61,17 @@ SWEEP = [(15, ["generic", "mfma", "valu"]), (16, ["generic"]), (17, ["generic", 
          (21, ["generic", "mfma", "valu"]), (31, ["generic"]), (8, ["valu"]), (2, ["mfma"])]
 
 
+# sweep draws at head_dim 64 and 256 with groups <= 4: the VALU kernel's other tile
+# geometries (32- and 8-token tiles), CSR and paged, one worker and many
+SWEEP_HEAD_DIMS = [0, 11, 28, 29, 36, 37]
+
+
+def test_valu_head_dims_in_bounds(asan_build):
+    cases = [{"sweep": s, "kernels": ["valu"]} for s in SWEEP_HEAD_DIMS]
+    rc, rows, err = _run(cases)
+    _assert_clean(rc, rows, err, len(SWEEP_HEAD_DIMS))
+
+
 def test_sweep_draws_in_bounds(asan_build):
     cases = [{"sweep": s, "kernels": k} for s, k in SWEEP]
     rc, rows, err = _run(cases)

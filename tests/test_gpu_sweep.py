@@ -56,8 +56,8 @@ def kernels_for(c, csr):
     ks = ["generic"]
     if c.head_dim == 128 and pow2:
         ks.append("mfma")
-        if c.group_size <= 4:
-            ks.append("valu")
+    if c.group_size <= 4 and pow2:  # the VALU kernel takes head_dim 64, 128 and 256
+        ks.append("valu")
     return ks
 
 

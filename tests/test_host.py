@@ -254,8 +254,16 @@ def test_attention_kernel_selection_is_host_only():
     assert b"group <= 4" in lib.sgd_last_error()
     args.kernel = _lib.KERNELS["mfma"]
     assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "mfma"
-    args.head_dim = 64  # head_dim 64: only the generic kernel
+    args.head_dim = 64  # group 8 at head_dim 64: the MFMA kernel takes head_dim 128 only
     assert lib.sgd_attention_kernel(ctypes.byref(args)) == -22
+    args.kernel = _lib.KERNELS["auto"]
+    assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "generic"
+    args.query_heads = 32  # group 4: the VALU kernel at every head_dim
+    for d in (64, 128, 256):
+        args.head_dim = d
+        args.k_stride[:] = [8 * d, 0, d, 1]
+        args.v_stride[:] = [8 * d, 0, d, 1]
+        assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "valu"
 
 
 # ------------------------------------------------------------------ engine host validation
