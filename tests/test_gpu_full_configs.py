@@ -4,11 +4,14 @@ defaults (AUTO kernel, two workers per CU), against the FP32 oracle (2e-2 abs / 
 * Llama-3-8B heads, batch 64, CSR page 1, lognormal lengths (median 1024): every schedule;
 * the skewed batch: 128 requests, 2 x 32768 + 126 x U[32, 512], up to 64 splits of at
   most 512 tokens: D1 and D4;
-* Llama-3-70B heads, batch 32, page 16, lengths U[2048, 16384]: D1 and D4, bf16 and fp16.
+* Llama-3-70B heads, batch 32, page 16, lengths U[2048, 16384]: every schedule in bf16,
+  D1 and D4 in fp16.
 
 Partials and LSEs are NaN-poisoned before each launch, the plan's error flag, record
 count and per-row counts are compared with the planning spec, and the per-layer claim
 counters must be back at zero afterwards (reference: tests/gpu/test_decode.py:12-39)."""
+import os
+
 import pytest
 import torch
 
@@ -39,7 +42,9 @@ def workload(name, dtype=torch.bfloat16):
             inputs = (q, k, v, indices)
         else:
             q, k, v, pages = W.make_inputs(c, lengths, seed=61, dtype=dtype)
-            expected = OA.paged_attention(q, k, v, pages, lengths, c.page_size)
+            threads = min(16, len(os.sched_getaffinity(0)))
+            expected = OA.paged_attention_threads(q.cpu(), k.cpu(), v.cpu(), pages.cpu(), lengths, c.page_size,
+                                                  threads=threads)
             inputs, indptr = (q, k, v, pages), None
         _CACHE[key] = (c, lengths, splits, inputs, indptr, expected)
     return _CACHE[key]
@@ -75,9 +80,12 @@ def test_skewed_batch128_every_request(mode):
     assert max(engine.plan.counts.tolist()) == 64  # the two long requests use all 64 splits
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("mode", [Mode.D1, Mode.D4])
-def test_llama70b_paged_batch32_every_request(mode, dtype):
+# every schedule in bf16, the claiming ones in fp16 too (grouped by dtype: one oracle each)
+C4_CASES = [(torch.bfloat16, m) for m in Mode] + [(torch.float16, Mode.D1), (torch.float16, Mode.D4)]
+
+
+@pytest.mark.parametrize("dtype,mode", C4_CASES, ids=[f"{str(d)[6:]}-{m.name}" for d, m in C4_CASES])
+def test_llama70b_paged_batch32_every_request(dtype, mode):
     engine = check("c4", mode, dtype)
     assert engine.attention_kernel_name() == "mfma"
 

@@ -1,5 +1,6 @@
 """hipGraph lifecycle: plan rebuilt on every replay, per-layer counters/scratch,
 stable pointers, shrink/regrow, device mode switching, capacity errors."""
+import os
 import pytest
 import torch
 
@@ -111,20 +112,31 @@ def _csr_step(fx, lengths):
     return indptrs, indices
 
 
-def _oracle_layer(x, indptr, indices, lengths):
-    """FP32 oracle on the rows the step uses, gathered on the device first."""
-    rows = indices.long()
-    k, v = x[1][rows].cpu(), x[2][rows].cpu()
-    local = torch.arange(rows.numel(), dtype=torch.int32)
-    return OA.csr_attention(x[0][:len(lengths)].cpu(), k, v, indptr.cpu(), local, lengths)
+def _oracle_layer_steps(x, steps, threads):
+    """FP32 oracle of one layer at every step: the layer's fixture rows (each request's
+    slots for its longest context) are copied to the host once, and each step's
+    (lengths, batch) reads a prefix of every request's rows there, on `threads` host
+    threads (oracle.attention.paged_attention_threads, pages of one token)."""
+    full_ptr = x[3].cpu().tolist()
+    rows = x[4].long()
+    k, v = x[1][rows].cpu()[:, None], x[2][rows].cpu()[:, None]  # [tokens, 1, Hkv, D]
+    q = x[0].cpu()
+    outs = []
+    for lengths in steps:
+        pages = torch.zeros((len(lengths), max(lengths)), dtype=torch.int64)
+        for r, n in enumerate(lengths):
+            pages[r, :n] = torch.arange(full_ptr[r], full_ptr[r] + n)
+        outs.append(OA.paged_attention_threads(q[:len(lengths)], k, v, pages, lengths, 1, threads=threads))
+    return outs
 
 
 def test_llama8b_32_layer_graph_shrinking_batches():
     """The 32-layer decode step under one hipGraph: 8B heads, batch 64 -> 48 -> 17 -> 1
     with contexts growing by one per step from a lognormal start (median 2048), the plan
     rebuilt on the device at every replay (a D4 rule for non-uniform batches; the uniform
-    batch-1 step takes the device bypass to R1), per-layer counters and scratch; the host
-    rejects an over-capacity step before touching the graph."""
+    batch-1 step takes the device bypass to R1), per-layer counters and scratch; every
+    layer of every step against the FP32 oracle; the host rejects an over-capacity step
+    before touching the graph."""
     c = W.config_for("c5")
     base = W.c5_lengths()
     layers = 32
@@ -137,7 +149,7 @@ def test_llama8b_32_layer_graph_shrinking_batches():
     key = PlanKey("c5", "hints", (c.query_heads, c.kv_heads, c.head_dim))
     graph = DecodeGraph(engine, [key] * layers, [(x[1], x[2]) for x in fx],
                         index_capacity=[x[4].numel() for x in fx])
-    checked = (0, 17, 31)
+    results, steps_lengths = [], []
     for step, batch in enumerate(W.C5_BATCHES):
         lengths = [x + step for x in base[:batch]]
         indptrs, indices = _csr_step(fx, lengths)
@@ -149,8 +161,14 @@ def test_llama8b_32_layer_graph_shrinking_batches():
         outs = graph.replay()
         torch.cuda.synchronize()
         assert engine.plan.mode.item() == (Mode.R1 if batch == 1 else Mode.D4)
-        for i in checked:
-            close(outs[i][:batch], _oracle_layer(fx[i], indptrs[i], indices[i], lengths)[:batch])
+        results.append([o[:batch].float().cpu() for o in outs])
+        steps_lengths.append(lengths)
+    threads = min(16, len(os.sched_getaffinity(0)))
+    for i in range(layers):
+        expected = _oracle_layer_steps(fx[i], steps_lengths, threads)
+        for step, lengths in enumerate(steps_lengths):
+            close(results[step][i], expected[step], msg=f"layer {i} step {step} batch {len(lengths)}")
+        print(f"layer {i}: {len(steps_lengths)} steps within tolerance", flush=True)
     # over capacity: the host refuses before the graph is touched
     with pytest.raises(ValueError):
         graph.update([x[0][:1] for x in fx], [x[4][:1] for x in fx], [c.max_context + 1], [1])
