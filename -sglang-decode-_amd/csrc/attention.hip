@@ -48,6 +48,7 @@ int check_args(const sgd_decode_args *args) {
         return einval("persistent_decode: null buffer");
     if (a.dispatch && a.dispatch_units < 0)
         return einval("persistent_decode: dispatch_units %d < 0", a.dispatch_units);
+    if (a.out && (reinterpret_cast<uintptr_t>(a.out) & 1)) return einval("persistent_decode: out not 2-byte aligned");
     return 0;
 }
 

@@ -54,6 +54,9 @@ __global__ __launch_bounds__(64 * kWaves) void k_attention_generic(sgd_decode_ar
         }
         __syncthreads();
         const int32_t length = a.lengths[t.request];
+        // a request's first split also writes its rows to `out` (final for a single-split
+        // request, overwritten by the merge otherwise)
+        const bool first = a.out != nullptr && t.split == 0;
         float m[GP], den[GP], acc[GP][DPL];
 #pragma unroll
         for (int j = 0; j < GP; ++j) {
@@ -182,6 +185,9 @@ __global__ __launch_bounds__(64 * kWaves) void k_attention_generic(sgd_decode_ar
 #pragma unroll
                 for (int w = 0; w < kWaves; ++w) x += sh.cacc[w][d] * sc[w];
                 a.partial[slot * D + d] = x / dd;
+                if (first)
+                    static_cast<uint16_t *>(a.out)[((int64_t)t.request * a.query_heads + t.group * G + j) * D + d] =
+                        (uint16_t)from_f32<DT>(x / dd);
             }
             if (threadIdx.x == 0) a.lse[slot] = mm + __logf(dd);
         }

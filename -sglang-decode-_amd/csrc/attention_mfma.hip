@@ -184,7 +184,7 @@ __device__ __forceinline__ void tile_compute(TileRegs &r, const uint4 (&q)[4], i
     }
 }
 
-template <int DT, bool CSR>
+template <int DT, bool CSR, bool kOut>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_args a) {
     extern __shared__ __align__(16) char dyn_smem[];
     MfmaShared &sh = *reinterpret_cast<MfmaShared *>(dyn_smem);
@@ -205,6 +205,10 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
         t.start = uni(ti.start);
         t.end = uni(ti.end);
         const int32_t split = uni(ti.split), group = uni(ti.group);
+        // kOut (sgd_decode_args.out set, a separate build): a request's first split also
+        // writes its rows to `out` (final for a single-split request, overwritten by the
+        // merge otherwise)
+        const bool first = kOut && split == 0;
         t.ind0 = CSR ? uni(a.indptr[t.request]) : 0;
         t.kbase = static_cast<const char *>(a.k) + group * (a.k_stride[2] * 2);
         t.vbase = static_cast<const char *>(a.v) + group * (a.v_stride[2] * 2);
@@ -306,22 +310,30 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
             const int64_t slot = ((int64_t)t.request * a.query_heads + group * G + h) * a.max_splits + split;
             a.partial[slot * kD + d] = acc / dd;
             if (d == 0) a.lse[slot] = (mm + __log2f(dd)) * kLn2;
+            if (first)
+                static_cast<uint16_t *>(a.out)[((int64_t)t.request * a.query_heads + group * G + h) * kD + d] =
+                    (uint16_t)from_f32<DT>(acc / dd);
         }
     }, sh.pf);
 }
 
-template <int DT, bool CSR>
-int launch_mfma_t(const sgd_decode_args &a, hipStream_t stream) {
+template <int DT, bool CSR, bool kOut>
+int launch_mfma_o(const sgd_decode_args &a, hipStream_t stream) {
     static bool attr = false;
     constexpr int bytes = (int)sizeof(MfmaShared);
     if (!attr) {
-        if (hipFuncSetAttribute((const void *)k_attention_mfma<DT, CSR>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                bytes) != hipSuccess)
+        if (hipFuncSetAttribute((const void *)k_attention_mfma<DT, CSR, kOut>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
             return einval("mfma attention: cannot reserve %d B of LDS", bytes);
         attr = true;
     }
-    hipLaunchKernelGGL((k_attention_mfma<DT, CSR>), dim3(a.workers), dim3(64 * kWaves), bytes, stream, a);
+    hipLaunchKernelGGL((k_attention_mfma<DT, CSR, kOut>), dim3(a.workers), dim3(64 * kWaves), bytes, stream, a);
     return launch_status("persistent_decode(mfma)");
+}
+
+template <int DT, bool CSR>
+int launch_mfma_t(const sgd_decode_args &a, hipStream_t stream) {
+    return a.out ? launch_mfma_o<DT, CSR, true>(a, stream) : launch_mfma_o<DT, CSR, false>(a, stream);
 }
 
 }  // namespace

@@ -47,7 +47,7 @@ struct ValuShared {
 };
 
 // ------------------------------------------------------------------ kernel
-template <int DT, bool CSR, int kWaves, int D>
+template <int DT, bool CSR, int kWaves, int D, bool kOut>
 __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_args a) {
     // 16 waves per CU (two 8-wave or one 16-wave workgroup): the load concurrency the
     // random row gathers need to approach the HBM ceiling (4 waves per SIMD, <= 128
@@ -99,6 +99,11 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
         T.start = uni(ti.start);
         T.end = uni(ti.end);
         const int32_t split = uni(ti.split), group = uni(ti.group);
+        // kOut (sgd_decode_args.out set): a request's first split also writes its normalized
+        // rows to `out` -- final for a single-split request, overwritten by the merge
+        // otherwise.  Testing split 0 needs no load of the request's length.  A separate
+        // build, so launches without `out` run the kernel without any of it.
+        const bool first = kOut && split == 0;
         T.ind0 = CSR ? uni(T.request < iptr_n ? sh.indptr[T.request] : a.indptr[T.request]) : 0;
         T.kbase = static_cast<const char *>(a.k) + group * (a.k_stride[2] * 2);
         T.vbase = static_cast<const char *>(a.v) + group * (a.v_stride[2] * 2);
@@ -202,23 +207,32 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
                 const int64_t slot = ((int64_t)T.request * a.query_heads + group * G + h) * a.max_splits + split;
                 a.partial[slot * D + d] = x / dd;
                 if (d == 0) a.lse[slot] = (mm + __log2f(dd)) * kLn2;
+                if (first)
+                    static_cast<uint16_t *>(a.out)[((int64_t)T.request * a.query_heads + group * G + h) * D + d] =
+                        (uint16_t)from_f32<DT>(x / dd);
             }
         }
     }, sh.pf);
 }
 
-template <int DT, bool CSR, int kWaves, int D>
-int launch_valu_w(const sgd_decode_args &a, hipStream_t stream) {
+template <int DT, bool CSR, int kWaves, int D, bool kOut>
+int launch_valu_o(const sgd_decode_args &a, hipStream_t stream) {
     static bool attr = false;
     const int bytes = (int)sizeof(ValuShared<kWaves, D>);
     if (!attr) {
-        if (hipFuncSetAttribute((const void *)k_attention_valu<DT, CSR, kWaves, D>,
+        if (hipFuncSetAttribute((const void *)k_attention_valu<DT, CSR, kWaves, D, kOut>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
             return einval("valu attention: cannot reserve %d B of LDS", bytes);
         attr = true;
     }
-    hipLaunchKernelGGL((k_attention_valu<DT, CSR, kWaves, D>), dim3(a.workers), dim3(64 * kWaves), bytes, stream, a);
+    hipLaunchKernelGGL((k_attention_valu<DT, CSR, kWaves, D, kOut>), dim3(a.workers), dim3(64 * kWaves), bytes, stream,
+                       a);
     return launch_status("persistent_decode(valu)");
+}
+
+template <int DT, bool CSR, int kWaves, int D>
+int launch_valu_w(const sgd_decode_args &a, hipStream_t stream) {
+    return a.out ? launch_valu_o<DT, CSR, kWaves, D, true>(a, stream) : launch_valu_o<DT, CSR, kWaves, D, false>(a, stream);
 }
 
 // Waves per workgroup from the environment variable SGD_VALU_WAVES (8 or 16, default 8:

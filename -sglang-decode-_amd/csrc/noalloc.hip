@@ -18,6 +18,8 @@
 #include "common.h"
 
 namespace sgd {
+int merge_rows_resident();  // merge.hip
+
 namespace {
 
 constexpr size_t kScratchBytes = size_t(32) << 20;
@@ -201,11 +203,15 @@ extern "C" int sgd_decode_noalloc(const sgd_noalloc_args *args, void *stream) {
     d.dtype = a.dtype;
     d.workers = a.workers;
     d.kernel = a.kernel;
+    // Beyond one residency round of merge rows, each request's first split also writes
+    // its rows and the merge takes only the multi-split ones (as DecodeEngine does).
+    const bool direct = (int64_t)a.batch_capacity * a.query_heads > merge_rows_resident();
+    d.out = direct ? a.out : nullptr;
     // Every refusal happens before the first device call: the attention's geometry and
     // kernel checks (the plan entry checks its own arguments before it launches).
     if (const int rc = sgd_attention_kernel(&d); rc < 0) return rc;
     if (int rc = sgd_build_plan(&p, a.force_mode, a.force_mode == 2, sync, 2, stream)) return rc;
     if (int rc = sgd_persistent_decode(&d, stream)) return rc;
-    return sgd_merge_splits(d.partial, d.lse, p.counts, a.active, p.error, a.out, a.batch_capacity,
-                            a.query_heads, a.head_dim, a.max_splits, a.dtype, stream);
+    return sgd_merge_splits_min(d.partial, d.lse, p.counts, a.active, p.error, a.out, a.batch_capacity,
+                                a.query_heads, a.head_dim, a.max_splits, direct ? 2 : 1, a.dtype, stream);
 }

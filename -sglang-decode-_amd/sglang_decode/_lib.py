@@ -40,7 +40,8 @@ class DecodeArgsC(ctypes.Structure):
         ("q_stride", ctypes.c_int64 * 3), ("k_stride", ctypes.c_int64 * 4),
         ("v_stride", ctypes.c_int64 * 4), ("pt_stride", ctypes.c_int64 * 2)] + [
         (name, _I) for name in ("query_heads", "kv_heads", "head_dim", "max_splits", "page_size",
-                                "csr", "dtype", "workers", "kernel", "dispatch_units")]
+                                "csr", "dtype", "workers", "kernel", "dispatch_units", "_pad1")] + [
+        ("out", _P)]
 
 
 class NoAllocArgsC(ctypes.Structure):
@@ -66,6 +67,7 @@ _SIGNATURES = {
     "sgd_persistent_decode": (_I, [ctypes.POINTER(DecodeArgsC), _P]),
     "sgd_attention_kernel": (_I, [ctypes.POINTER(DecodeArgsC)]),
     "sgd_merge_splits": (_I, [_P] * 6 + [_I] * 5 + [_P]),
+    "sgd_merge_splits_min": (_I, [_P] * 6 + [_I] * 6 + [_P]),
     "sgd_host_static_lists": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "sgd_host_static_plan": (_I, [_P, _P] + [_I] * 7 + [_P, _P, _P]),
     "sgd_decode_noalloc": (_I, [ctypes.POINTER(NoAllocArgsC), _P]),

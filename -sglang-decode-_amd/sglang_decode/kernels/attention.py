@@ -55,7 +55,10 @@ def checked_layout(config, q, k, v, pages, indptr, out_dtype=None, who="execute"
 
 
 def persistent_decode(plan, layer, q, k, v, pages, indptr, scale, k_strides, v_strides,
-                      pt_strides, csr, kernel="auto"):
+                      pt_strides, csr, kernel="auto", write_single=False):
+    """One attention launch.  ``write_single``: the tasks that are their request's only
+    split also write their row of ``layer.output`` (contiguous [Bcap, Hq, D] in q's dtype),
+    so the merge may skip those rows (kernels.merge.merge_splits with min_splits 2)."""
     c = plan.config
     a = DecodeArgsC()
     a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
@@ -82,6 +85,8 @@ def persistent_decode(plan, layer, q, k, v, pages, indptr, scale, k_strides, v_s
     a.dtype = _lib.dtype_code(q.dtype)
     a.workers = c.workers
     a.kernel = _lib.KERNELS[kernel] if isinstance(kernel, str) else int(kernel)
+    if write_single:
+        a.out = layer.output.data_ptr()
     check(_lib.lib().sgd_persistent_decode(ctypes.byref(a), _lib.stream_handle(q.device)),
           "persistent_decode")
     return _lib.KERNEL_NAMES[_lib.lib().sgd_attention_kernel(ctypes.byref(a))]

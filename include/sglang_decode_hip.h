@@ -190,6 +190,13 @@ typedef struct sgd_decode_args {
     int32_t kernel;                 /* enum sgd_kernel */
     int32_t dispatch_units;         /* entries in dispatch; units at or beyond it resolve through
                                        the plan arrays */
+    int32_t _pad1;
+    void *out;                      /* optional (may be NULL): [bcap, Hq, D] in `dtype`, contiguous.
+                                       Every split-0 task also writes its normalized output here,
+                                       rounded to dtype.  For a single-split request these are the
+                                       bits sgd_merge_splits would write for the row, so
+                                       sgd_merge_splits_min(min_splits = 2) can leave it alone; the
+                                       other rows hold a split's output until the merge writes them. */
 } sgd_decode_args;
 
 /*
@@ -223,6 +230,19 @@ int sgd_merge_splits(const float *partial, const float *lse, const int32_t *coun
                      const int32_t *active, const int32_t *error, void *out, int32_t bcap,
                      int32_t query_heads, int32_t head_dim, int32_t max_splits, int32_t dtype,
                      void *stream);
+
+/*
+ * sgd_merge_splits for the rows that need a merge: rows whose request has 1 <= counts[r]
+ * < min_splits are left untouched (the attention wrote them through sgd_decode_args.out);
+ * rows without splits still get 0 and *error != 0 still writes NaN everywhere.
+ * min_splits <= 1 is sgd_merge_splits.  No reference counterpart: the reference merges
+ * every row (kernels/merge.py:7-30); with min_splits 2 a batch of mostly single-split
+ * requests leaves only its multi-split rows to this launch.
+ */
+int sgd_merge_splits_min(const float *partial, const float *lse, const int32_t *counts,
+                         const int32_t *active, const int32_t *error, void *out, int32_t bcap,
+                         int32_t query_heads, int32_t head_dim, int32_t max_splits, int32_t min_splits,
+                         int32_t dtype, void *stream);
 
 /*
  * The decode step's writes around the attention, one launch per layer.  Replaces the
@@ -309,7 +329,8 @@ typedef struct sgd_noalloc_args {
 
 /*
  * One decode step that allocates nothing: sgd_build_plan (no policy rules, block_kv
- * 128), sgd_persistent_decode and sgd_merge_splits on `stream`, with the plan and
+ * 128), sgd_persistent_decode (single-split rows written straight to `out`) and
+ * sgd_merge_splits_min (min_splits 2) on `stream`, with the plan and
  * dispatch tables, the claim counters and the split partial/LSE slots in a static
  * device array of 32 MiB held by the library on every GPU it runs on.  No counterpart
  * in the reference: for callers that cannot call hipMalloc (code under HIP graph

@@ -5,8 +5,9 @@ clang's ASan runtime preloaded, which ``run_case.py`` arranges in a child proces
 Device buffers are host allocations of exactly the size a device buffer would have,
 filled with garbage like fresh device memory, so AddressSanitizer sees every access
 past a buffer's end.  ``decode()`` makes the calls DecodeEngine.prepare()/execute()
-make -- the fused plan build with the layer's counters, the attention launch and the
-split merge -- with the same argument marshalling.
+make -- the fused plan build with the layer's counters, the attention launch (writing
+single-split rows to the output) and the split merge of the other rows -- with the same
+argument marshalling.
 """
 import ctypes
 import os
@@ -120,7 +121,7 @@ class Plan:
 
 
 def decode(emu, config, lengths, splits, q, k, v, pages, indptr=None, *, mode=-1, kernel="auto", scale=None,
-           rules=(), run_greedy=None, poison=True):
+           rules=(), run_greedy=None, poison=True, direct=True):
     """One prepare() + execute() on the executor.  q/k/v: torch CPU tensors (bf16/fp16);
     pages: paged table [Bcap, max_pages] or CSR kv_indices; indptr: CSR kv_indptr or None.
     Returns dict(out [Bcap,Hq,D] float32, partial, lse, plan, kernel)."""
@@ -137,7 +138,7 @@ def decode(emu, config, lengths, splits, q, k, v, pages, indptr=None, *, mode=-1
     shape = (c.batch_capacity, c.query_heads, c.max_splits)
     partial = emu.array((*shape, c.head_dim), np.float32, np.nan if poison else None)
     lse = emu.array(shape, np.float32, np.nan if poison else None)
-    out = emu.array((c.batch_capacity, c.query_heads, c.head_dim), np.uint16)
+    out = emu.array((c.batch_capacity, c.query_heads, c.head_dim), np.uint16, 0x7fc0 if poison else None)
     if run_greedy is None:
         run_greedy = int(mode) == 2 or any(int(r.mode) == 2 for r in rules)
     emu.check(emu.lib.sgd_build_plan(ctypes.byref(plan.c_struct()), int(mode), int(bool(run_greedy)),
@@ -167,10 +168,12 @@ def decode(emu, config, lengths, splits, q, k, v, pages, indptr=None, *, mode=-1
     a.query_heads, a.kv_heads, a.head_dim = c.query_heads, c.kv_heads, c.head_dim
     a.max_splits, a.page_size, a.dtype, a.workers = c.max_splits, c.page_size, dt, c.workers
     a.kernel = _lib.KERNELS[kernel]
+    if direct:  # single-split rows straight from the attention, as DecodeEngine.execute does
+        a.out = out.ctypes.data
     emu.check(emu.lib.sgd_persistent_decode(ctypes.byref(a), None), "persistent_decode")
     ran = _lib.KERNEL_NAMES[emu.lib.sgd_attention_kernel(ctypes.byref(a))]
-    emu.check(emu.lib.sgd_merge_splits(
+    emu.check(emu.lib.sgd_merge_splits_min(
         ptr(partial), ptr(lse), ptr(plan.counts), ptr(plan.active), ptr(plan.error), ptr(out),
-        c.batch_capacity, c.query_heads, c.head_dim, c.max_splits, dt, None), "merge_splits")
+        c.batch_capacity, c.query_heads, c.head_dim, c.max_splits, 2 if direct else 1, dt, None), "merge_splits")
     return dict(out=from_bits16(out, dt).reshape(out.shape), partial=np.array(partial), lse=np.array(lse),
                 plan=plan.read(), kernel=ran, sync=sync.tolist())

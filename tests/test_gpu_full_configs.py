@@ -113,3 +113,39 @@ def test_llama8b_batch64_host_static_every_request():
         assert engine.plan.static_head.tolist() == heads
         assert engine.plan.static_next.tolist() == links
         close(out[:len(lengths)], expected[:len(lengths)], msg="c2 STATIC_HOST")
+
+
+@pytest.mark.parametrize("name,kernel", [("c2", "auto"), ("c3", "auto"), ("c4", "auto"), ("c2", "generic")])
+def test_single_split_rows_from_the_attention_equal_the_merge(name, kernel):
+    """With direct first-split writes (the engine's choice when the merge rows outnumber one
+    residency round, C3 here; forced on for the others) each request's first split also
+    writes its rows and the merge takes only the multi-split ones (sgd_merge_splits_min,
+    min_splits 2).  Bit for bit the same output as the reference's order -- every split to
+    its slot, every row merged (sgd_merge_splits) -- on each kernel; the split slots are
+    still all written."""
+    from sglang_decode.kernels.attention import checked_layout, persistent_decode
+    from sglang_decode.kernels.merge import merge_splits
+    c, lengths, splits, inputs, indptr, expected = workload(name)
+    engine = DecodeEngine(c, force_mode=Mode.D1, kernel=kernel)
+    assert engine.direct_first_split == (name == "c3")  # 4096 merge rows > 8 per CU x 256 CUs
+    engine.direct_first_split = True
+    W.update_plan(engine, lengths, splits)
+    engine.prepare()
+    layer = engine.layers[0]
+    layer.output.fill_(float("nan"))
+    layer.partial.fill_(float("nan"))
+    direct = engine.execute(*inputs, indptr=indptr).clone()
+    slots = layer.partial.clone()
+    records, counts, _ = split_records(lengths, splits, c)
+    assert name == "c4" or sum(1 for n in counts if n == 1) > 0  # c4: every request has several splits
+    layer.output.fill_(float("nan"))
+    layer.partial.fill_(float("nan"))
+    ks, vs, pts, csr = checked_layout(c, *inputs, indptr, layer.output.dtype)
+    persistent_decode(engine.plan, layer, *inputs, indptr, c.head_dim ** -0.5, ks, vs, pts, csr, kernel,
+                      write_single=False)
+    merge_splits(engine.plan, layer, min_splits=1)
+    torch.cuda.synchronize()
+    n = len(lengths)
+    assert torch.equal(direct[:n].view(torch.int16), layer.output[:n].view(torch.int16)), name
+    assert torch.equal(slots.view(torch.int32), layer.partial.view(torch.int32))
+    close(direct[:n], expected[:n], msg=f"{name} {kernel}")
