@@ -217,6 +217,38 @@ def _noalloc(emu, name, batches, mode, dtype):
     return dict(case="noalloc", workload=name, mode=int(mode), calls=rows)
 
 
+def _merge_min(emu, bcap, hq, smax, d, min_splits):
+    """sgd_merge_splits_min against sgd_merge_splits on synthetic split slots: rows of
+    1 <= n < min_splits untouched, every other row bitwise equal, a plan error NaN
+    everywhere.  The executor reports one workgroup per CU as resident, so batches of more
+    rows than CUs stride."""
+    import ctypes
+    import numpy as np
+    import driver as D
+    from sglang_decode import _lib
+    rng = np.random.default_rng(5)
+    counts = emu.upload(np.array([(0, 1, 2, 16, 17, 64, 1, 3)[r % 8] % (smax + 1) for r in range(bcap)], np.int32))
+    partial = emu.upload(rng.standard_normal((bcap, hq, smax, d)).astype(np.float32))
+    lse = emu.upload((rng.standard_normal((bcap, hq, smax)) * 3).astype(np.float32))
+    active = emu.upload(np.array([bcap], np.int32))
+    res = {}
+    for tag, m, error in (("full", None, 0), ("min", min_splits, 0), ("error", min_splits, 1)):
+        out = emu.array((bcap, hq, d), np.uint16, 0x40e0)  # 7.0 in bf16
+        err = emu.upload(np.array([error], np.int32))
+        args = (D.ptr(partial), D.ptr(lse), D.ptr(counts), D.ptr(active), D.ptr(err), D.ptr(out), bcap, hq, d, smax)
+        if m is None:
+            emu.check(emu.lib.sgd_merge_splits(*args, _lib.SGD_BF16, None), "merge_splits")
+        else:
+            emu.check(emu.lib.sgd_merge_splits_min(*args, m, _lib.SGD_BF16, None), "merge_splits_min")
+        res[tag] = np.array(out)
+    n = np.array(counts)
+    skip = (n >= 1) & (n < min_splits)
+    return dict(case="merge_min", rows=bcap * hq, min_splits=min_splits,
+                merged_equal=bool(np.array_equal(res["min"][~skip], res["full"][~skip])),
+                skipped_untouched=bool((res["min"][skip] == 0x40e0).all()),
+                error_nan=bool(np.isnan(D.from_bits16(res["error"], _lib.SGD_BF16)).all()))
+
+
 def run(cases, asan):
     import torch
     import driver as D
@@ -229,6 +261,9 @@ def run(cases, asan):
             lengths, smax = case["upstream"]
             print(json.dumps(_upstream(emu, list(lengths), int(smax), getattr(torch, case.get("dtype", "bfloat16")))),
                   flush=True)
+        elif "merge_min" in case:
+            bcap, hq, smax, d, m = case["merge_min"]
+            print(json.dumps(_merge_min(emu, int(bcap), int(hq), int(smax), int(d), int(m))), flush=True)
         elif "noalloc" in case:
             print(json.dumps(_noalloc(emu, case["noalloc"], case["batches"], int(case.get("mode", -1)),
                                       getattr(torch, case.get("dtype", "bfloat16")))), flush=True)

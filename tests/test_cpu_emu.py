@@ -72,6 +72,18 @@ def test_valu_head_dims_in_bounds(asan_build):
     _assert_clean(rc, rows, err, len(SWEEP_HEAD_DIMS))
 
 
+def test_selective_merge_strides_in_bounds(asan_build):
+    """sgd_merge_splits_min with more rows than resident workgroups (the executor reports
+    one per CU, 256 here; 512 rows) at every head dim: merged rows bitwise equal to
+    sgd_merge_splits, skipped rows untouched, NaN on a plan error, all in bounds."""
+    cases = [{"merge_min": [64, 8, 64, d, 2]} for d in (64, 128, 256)] + [{"merge_min": [64, 8, 16, 128, 17]}]
+    rc, rows, err = _run(cases)
+    assert rc == 0 and "ERROR: AddressSanitizer" not in err, err[-4000:]
+    assert len(rows) == len(cases), err[-2000:]
+    for r in rows:
+        assert r["merged_equal"] and r["skipped_untouched"] and r["error_nan"], r
+
+
 def test_sweep_draws_in_bounds(asan_build):
     cases = [{"sweep": s, "kernels": k} for s, k in SWEEP]
     rc, rows, err = _run(cases)

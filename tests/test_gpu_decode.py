@@ -232,3 +232,44 @@ def test_rows_with_many_splits(csr, dtype):
     assert max(counts) == 64 and sum(n > 16 for n in counts) == 4  # the multi-wave path runs
     close(out[:len(lengths)], exp[:len(lengths)])
     assert not out[len(lengths):].float().abs().sum().item()
+
+
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+def test_merge_splits_min_rows_and_grid(head_dim):
+    """sgd_merge_splits_min at the C ABI on synthetic split slots: rows of requests with 1 <=
+    n < min_splits are left as they were, every other row is bitwise what sgd_merge_splits
+    writes (rows of 0 splits: zeros), and a plan error writes NaN everywhere.  The batch's
+    rows (256 x 32) exceed one residency round, so the kernel strides; its rows mix 0, 1,
+    2, 16, 17 and 64 splits."""
+    from sglang_decode import _lib
+    from sglang_decode._lib import ptr
+    lib = _lib.lib()
+    bcap, hq, smax, d = 256, 32, 64, head_dim
+    g = torch.Generator().manual_seed(7)
+    counts = torch.tensor([(0, 1, 2, 16, 17, 64, 1, 1)[r % 8] for r in range(bcap)], dtype=torch.int32)
+    partial = torch.randn(bcap, hq, smax, d, generator=g).cuda()
+    lse = (torch.randn(bcap, hq, smax, generator=g) * 3).cuda()
+    counts_d, active = counts.cuda(), torch.tensor([bcap], dtype=torch.int32).cuda()
+    stream = _lib.stream_handle(partial.device)
+
+    def merge(min_splits, error):
+        out = torch.full((bcap, hq, d), 7.0, dtype=torch.bfloat16, device="cuda")
+        err = torch.tensor([error], dtype=torch.int32).cuda()
+        args = (ptr(partial), ptr(lse), ptr(counts_d), ptr(active), ptr(err), ptr(out), bcap, hq, d, smax)
+        if min_splits is None:
+            rc = lib.sgd_merge_splits(*args, _lib.SGD_BF16, stream)
+        else:
+            rc = lib.sgd_merge_splits_min(*args, min_splits, _lib.SGD_BF16, stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        return out
+
+    full = merge(None, 0)
+    for m in (1, 2, 17, 65):
+        part = merge(m, 0)
+        skipped = (counts >= 1) & (counts < m)
+        assert torch.equal(part[~skipped].view(torch.int16), full[~skipped].view(torch.int16)), m
+        assert (part[skipped].float() == 7.0).all(), m
+    assert not full[counts == 0].float().abs().sum().item()
+    assert torch.isnan(merge(2, 1).float()).all()
+    assert torch.equal(merge(1, 0).view(torch.int16), full.view(torch.int16))
