@@ -33,6 +33,17 @@ int einval(const char *fmt, ...) {
 
 void clear_stale_error() { (void)hipGetLastError(); }
 
+int set_dynamic_lds(const void *kernel, int bytes, bool *done, const char *what) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    const bool cached = dev >= 0 && dev < kOnceDevices;
+    if (cached && done[dev]) return 0;
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
+        return einval("%s: cannot reserve %d B of LDS", what, bytes);
+    if (cached) done[dev] = true;
+    return 0;
+}
+
 int launch_status(const char *what) {
     const hipError_t e = hipGetLastError();
     if (e == hipSuccess) return 0;

@@ -319,14 +319,10 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
 
 template <int DT, bool CSR, bool kOut>
 int launch_mfma_o(const sgd_decode_args &a, hipStream_t stream) {
-    static bool attr = false;
+    static bool attr[kOnceDevices] = {};
     constexpr int bytes = (int)sizeof(MfmaShared);
-    if (!attr) {
-        if (hipFuncSetAttribute((const void *)k_attention_mfma<DT, CSR, kOut>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
-            return einval("mfma attention: cannot reserve %d B of LDS", bytes);
-        attr = true;
-    }
+    if (int rc = set_dynamic_lds((const void *)k_attention_mfma<DT, CSR, kOut>, bytes, attr, "mfma attention"))
+        return rc;
     hipLaunchKernelGGL((k_attention_mfma<DT, CSR, kOut>), dim3(a.workers), dim3(64 * kWaves), bytes, stream, a);
     return launch_status("persistent_decode(mfma)");
 }

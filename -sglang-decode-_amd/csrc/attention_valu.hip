@@ -217,14 +217,11 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
 
 template <int DT, bool CSR, int kWaves, int D, bool kOut>
 int launch_valu_o(const sgd_decode_args &a, hipStream_t stream) {
-    static bool attr = false;
+    static bool attr[kOnceDevices] = {};
     const int bytes = (int)sizeof(ValuShared<kWaves, D>);
-    if (!attr) {
-        if (hipFuncSetAttribute((const void *)k_attention_valu<DT, CSR, kWaves, D, kOut>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
-            return einval("valu attention: cannot reserve %d B of LDS", bytes);
-        attr = true;
-    }
+    if (int rc = set_dynamic_lds((const void *)k_attention_valu<DT, CSR, kWaves, D, kOut>, bytes, attr,
+                                 "valu attention"))
+        return rc;
     hipLaunchKernelGGL((k_attention_valu<DT, CSR, kWaves, D, kOut>), dim3(a.workers), dim3(64 * kWaves), bytes, stream,
                        a);
     return launch_status("persistent_decode(valu)");

@@ -17,6 +17,12 @@ int einval(const char *fmt, ...);
 int launch_status(const char *what);
 void clear_stale_error();
 
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once per device:
+// `done` is the kernel's flag array (kOnceDevices entries, zero-initialised); devices past
+// it are set on every call.  SGD_EINVAL naming `what` if the runtime refuses.
+constexpr int kOnceDevices = 64;
+int set_dynamic_lds(const void *kernel, int bytes, bool *done, const char *what);
+
 // ------------------------------------------------------------------ device side
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {

@@ -14,7 +14,9 @@
 namespace sgd {
 
 // Rows the full merge (k_merge: one 4-wave workgroup per row, 60 VGPRs, so 8 per CU)
-// keeps resident at once on the current device; beyond them its workgroups queue in rounds.
+// keeps resident at once; beyond them its workgroups queue in rounds.  Read once per
+// process from the first device used (a node's GPUs are alike); it only chooses between
+// two correct merge orders and sizes a strided grid, so any value is safe.
 int merge_rows_resident() {
     static int rows = [] {
         int dev = 0, cus = 0;

@@ -663,17 +663,12 @@ __global__ __launch_bounds__(kPlanThreads) void k_build_plan(sgd_plan_buffers p,
     }
 }
 
-bool lds_attr_set = false;
+bool greedy_attr[kOnceDevices] = {}, build_attr[kOnceDevices] = {};
 
 int prepare_plan_launch() {
-    if (lds_attr_set) return 0;
-    if (hipFuncSetAttribute((const void *)k_greedy_lists, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)sizeof(GreedyShared)) != hipSuccess ||
-        hipFuncSetAttribute((const void *)k_build_plan, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)sizeof(FusedLds)) != hipSuccess)
-        return einval("hipFuncSetAttribute(max dynamic LDS) failed");
-    lds_attr_set = true;
-    return 0;
+    if (int rc = set_dynamic_lds((const void *)k_greedy_lists, (int)sizeof(GreedyShared), greedy_attr, "greedy_lists"))
+        return rc;
+    return set_dynamic_lds((const void *)k_build_plan, (int)sizeof(FusedLds), build_attr, "build_plan");
 }
 
 int check_plan_geometry(int32_t bcap, int32_t smax, int32_t hkv, int32_t workers, int32_t buckets) {

@@ -168,14 +168,9 @@ __global__ __launch_bounds__(64) void k_upstream_merge(const float *__restrict__
 template <int DT>
 int launch_upstream(const sgd_decode_args &a, const int32_t *num_splits, void *out, int32_t batch,
                     hipStream_t stream) {
-    static bool attr = false;
+    static bool attr[kOnceDevices] = {};
     const int bytes = (int)sizeof(UpShared);
-    if (!attr) {
-        if (hipFuncSetAttribute((const void *)k_upstream_split<DT>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                bytes) != hipSuccess)
-            return einval("upstream_decode: cannot reserve %d B of LDS", bytes);
-        attr = true;
-    }
+    if (int rc = set_dynamic_lds((const void *)k_upstream_split<DT>, bytes, attr, "upstream_decode")) return rc;
     hipLaunchKernelGGL(k_upstream_split<DT>, dim3(a.max_splits, a.kv_heads, batch), dim3(64 * kUpWaves), bytes,
                        stream, a, num_splits);
     if (int rc = launch_status("upstream_decode(stage 1)")) return rc;
