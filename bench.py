@@ -29,6 +29,11 @@ device plan; `default_schedule` names the artifact and the mode its rules picked
 `value` is the achieved HBM GB/s of the fastest schedule.
 `roofline` times the attention kernel alone for that schedule: a HIP graph of
 back-to-back launches (rotating layers) replayed between HIP events on its stream.
+`roofline.traffic` is the HBM bytes per attention launch from two rocprofv3 --pmc passes
+(FETCH_SIZE, then WRITE_SIZE) run by this bench in child processes over the same workload,
+each scaled by the counter's reading for a copy kernel of known size in the same pass
+(`--traffic file` or a failed pass: the committed profiles' lookup, named in
+`traffic_source`).
 `attention_merge_us` (attention + merge per layer, no plan) and `single_layer_entry_us`
 (one layer's full entry: plan build + attention + merge) are timed the same way for that
 schedule; `entry` times that full entry per schedule at the reference's own boundary:
@@ -109,7 +114,108 @@ def parse():
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "traffic_persistent_decode.json"),
                     help="measured HBM bytes per attention launch (from rocprofv3 --pmc), used for "
                          "roofline.traffic when kernel, schedule and workers match this run")
+    ap.add_argument("--traffic", default="live", choices=("live", "file", "off"),
+                    help="roofline.traffic: live = two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over "
+                         "the reported schedule's attention launches in child processes, scaled by a copy "
+                         "kernel in the same passes (falls back to --traffic-file if rocprofv3 fails); "
+                         "file = the --traffic-file lookup only")
+    ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     return ap.parse_args()
+
+
+COPY_MIB = 256
+
+
+def traffic_child(args):
+    """The workload of one live traffic pass (run under rocprofv3 --pmc by the parent): the
+    reported schedule's attention launches on one KV pool, then a plain copy kernel of
+    COPY_MIB MiB read + written 5 times, whose counts give the counter's bytes scale."""
+    import torch
+    from sglang_decode import workloads as W
+    from sglang_decode.config import Mode
+    from sglang_decode.kernels.attention import checked_layout, persistent_decode
+    from sglang_decode.runtime.engine import DecodeEngine
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    dtype = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    c = W.config_for(args.workload, workers=args.workers)
+    if args.head_dim:
+        import dataclasses
+        c = dataclasses.replace(c, head_dim=args.head_dim)
+    lengths = W.lengths_for(args.workload)
+    splits = W.split_hints(lengths, c.max_splits)
+    csr = c.page_size == 1
+    if csr:
+        x = W.make_csr_inputs(c, lengths, seed=1000, device=dev, dtype=dtype, device_pool=True,
+                              pool_tokens=1 << (18 if args.workload == "c5" else 20))
+        inputs, indptr = (x[0], x[1], x[2], x[4]), x[3]
+    else:
+        x = W.make_inputs(c, lengths, seed=1000, device=dev, dtype=dtype, pool_pages=200_000, device_pool=True)
+        inputs, indptr = x, None
+    engine = DecodeEngine(c, device=dev, dtype=dtype, force_mode=int(Mode[args.policies]), kernel=args.kernel)
+    W.update_plan(engine, lengths, splits)
+    engine.prepare()
+    ks, vs, pts, _ = checked_layout(c, *inputs, indptr, dtype)
+    for _ in range(5):
+        persistent_decode(engine.plan, engine.layers[0], *inputs, indptr, c.head_dim ** -0.5, ks, vs, pts, csr,
+                          args.kernel)
+    a = torch.empty(COPY_MIB << 19, dtype=torch.bfloat16, device=dev).fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(5):
+        torch.mul(a, 1, out=b)
+    torch.cuda.synchronize()
+
+
+def live_traffic(args, schedule, workers):
+    """HBM bytes per attention launch of this run's workload and schedule from two rocprofv3
+    --pmc passes (FETCH_SIZE, WRITE_SIZE) over traffic_child, each scaled by what the same
+    counter reads for the copy kernel of known size; None if rocprofv3 is missing or a pass
+    yields no counts (bounded by a time limit, its process group killed on expiry)."""
+    import csv
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+    tool = shutil.which("rocprofv3")
+    profiled = any(k.startswith("ROCPROF") for k in os.environ) or "rocprof" in os.environ.get("LD_PRELOAD", "")
+    if tool is None or profiled:  # no profiler, or this run is itself under one
+        return None
+    child = [sys.executable, os.path.abspath(__file__), "--traffic-child", "--workload", args.workload,
+             "--dtype", args.dtype, "--kernel", args.kernel, "--policies", schedule, "--workers", str(workers),
+             "--head-dim", str(args.head_dim)]
+    env = dict(os.environ, TMPDIR="/tmp")
+    counts = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = tempfile.mkdtemp(prefix="sgd_pmc_", dir="/tmp")
+        cmd = [tool, "--pmc", counter, "-d", out, "-o", "run", "--output-format", "csv", "--", *child]
+        proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                                start_new_session=True)
+        try:
+            proc.wait(timeout=240)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.wait()
+        attn, copy = [], []
+        for root, _, files in os.walk(out):
+            for name in files:
+                if not name.endswith("counter_collection.csv"):
+                    continue
+                with open(os.path.join(root, name), newline="") as f:
+                    for row in csv.DictReader(f):
+                        kernel = row.get("Kernel_Name", "")
+                        if "k_attention_" in kernel:
+                            attn.append(float(row["Counter_Value"]))
+                        elif "MulFunctor" in kernel:
+                            copy.append(float(row["Counter_Value"]))
+        shutil.rmtree(out, ignore_errors=True)
+        if not attn or not copy:  # the profiler's own exit code is not trusted either way
+            return None
+        factor = (sum(copy) / len(copy)) * 1024.0 / (COPY_MIB << 20)
+        counts[counter] = (sum(attn) / len(attn)) * 1024.0 / factor, factor
+    read, fetch_factor = counts["FETCH_SIZE"]
+    written, write_factor = counts["WRITE_SIZE"]
+    return dict(read_bytes=round(read), write_bytes=round(written), traffic_bytes=round(read + written),
+                fetch_factor=round(fetch_factor, 5), write_factor=round(write_factor, 5))
 
 
 def measured_traffic(path, kernel, workers, algorithmic_bytes):
@@ -369,6 +475,9 @@ def provenance(dev, args, config, lengths, splits):
 
 def main():
     args = parse()
+    if args.traffic_child:
+        traffic_child(args)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the decode path "
               "has no collective; each GPU would run its own share of the batch or of the KV heads)",
@@ -602,9 +711,9 @@ def main():
     kern_us = statistics.median(durs)
     achieved = bytes_per_layer / (kern_us * 1e-6) / 1e9
     kernel_name = engine.attention_kernel_name()
+    # traffic and traffic_source are filled in after every timed leg (live_traffic)
     roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                    frac=round(achieved / PEAK_HBM_GBS, 4),
-                    traffic=measured_traffic(args.traffic_file, kernel_name, workers, bytes_per_layer),
+                    frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None, traffic_source=None,
                     attention_kernel=kernel_name,
                     kernel="persistent_decode", kernel_us=round(kern_us, 2),
                     algorithmic_bytes=bytes_per_layer)
@@ -759,6 +868,23 @@ def main():
                                "same lengths, one thread, median of 5 after 1 warmup")
         print(f"[bench] cpu baseline: {t * 1e3:.1f} ms/layer on {cpu_threads} threads; planning spec "
               f"{plan_t * 1e6:.0f} us", flush=True)
+
+    # the live traffic passes last: their child processes run under the profiler after every
+    # timed leg of this run is done
+    if args.traffic == "live":
+        # the bytes do not depend on the schedule (it only changes which worker reads which
+        # rows); schedules that are not a device mode are counted as D1
+        live = live_traffic(args, "D1" if best in ("AUTO", "STATIC_HOST") else best, workers)
+        if live is not None:
+            roofline["traffic"] = live["traffic_bytes"]
+            roofline["traffic_source"] = dict(kind="rocprofv3 --pmc in this run", **live)
+            print(f"[bench] live HBM traffic per attention launch: {live['read_bytes'] / 1e6:.2f} MB read + "
+                  f"{live['write_bytes'] / 1e6:.2f} MB written (FETCH_SIZE scale {live['fetch_factor']})",
+                  flush=True)
+    if roofline["traffic"] is None and args.traffic != "off":
+        roofline["traffic"] = measured_traffic(args.traffic_file, kernel_name, workers, bytes_per_layer)
+        if roofline["traffic"] is not None:
+            roofline["traffic_source"] = dict(kind="file", path=os.path.relpath(args.traffic_file, ROOT))
 
     r = results[best]
     line = {
