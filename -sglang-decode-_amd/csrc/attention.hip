@@ -68,12 +68,12 @@ int resolve_kernel(const sgd_decode_args &a) {
             return SGD_KERNEL_GENERIC;
         case SGD_KERNEL_VALU:
             if (!valu_supported(a))
-                return einval("persistent_decode: the VALU kernel needs group <= 4, head_dim 128, unit dim "
+                return einval("persistent_decode: the VALU kernel needs group <= 4, head_dim 64/128/256, unit dim "
                               "stride, 16-byte aligned rows and a power-of-two page size");
             return SGD_KERNEL_VALU;
         case SGD_KERNEL_MFMA:
             if (!mfma_supported(a))
-                return einval("persistent_decode: the MFMA kernel needs group <= 16, head_dim 128, unit dim "
+                return einval("persistent_decode: the MFMA kernel needs group <= 16, head_dim 64/128/256, unit dim "
                               "stride, 16-byte aligned rows and a power-of-two page size");
             return SGD_KERNEL_MFMA;
         default:

@@ -251,14 +251,15 @@ void resolve_wave(Block &b, int w0, int w1) {
     if (kind == X_MFMA) {
         for (int l = 0; l < kWave; ++l)
             if (!active(l)) fatal("kernel %s: MFMA (line %d) with inactive lane %d", b.kernel, line, l);
+        const int K = ops[first]->p0, per = K / 4;  // k elements per lane group: 8 (K 32) or 4 (K 16)
         for (int l = 0; l < kWave; ++l) {
             const int n = l & 15, j = l >> 4;
             for (int i = 0; i < 4; ++i) {
                 const int m = 4 * j + i;
                 double acc = ops[l]->c[i];
-                for (int k = 0; k < 32; ++k) {
-                    const XOp &A = *ops[m + 16 * (k >> 3)], &B = *ops[n + 16 * (k >> 3)];
-                    const int e = k & 7;
+                for (int k = 0; k < K; ++k) {
+                    const XOp &A = *ops[m + 16 * (k / per)], &B = *ops[n + 16 * (k / per)];
+                    const int e = k % per;
                     const float av = cvt16(ops[l]->dt, (A.a[e >> 1] >> (16 * (e & 1))) & 0xffff);
                     const float bv = cvt16(ops[l]->dt, (B.b[e >> 1] >> (16 * (e & 1))) & 0xffff);
                     acc += (double)av * bv;

@@ -171,9 +171,30 @@ inline VC mfma_16x16x32(int dt, VA a, VA b, VC c, int line) {
     op.kind = X_MFMA;
     op.dt = dt;
     op.bytes = 16;
+    op.p0 = 32;  // K
     op.line = line;
     memcpy(op.a, &a, 16);
     memcpy(op.b, &b, 16);
+    memcpy(op.c, &c, 16);
+    cross_lane(op);
+    VC d;
+    memcpy(&d, op.d, 16);
+    return d;
+}
+
+// v_mfma_f32_16x16x16_{bf16,f16}: lane l = (l % 16, l / 16) holds A[m][4j..4j+3],
+// B[4j..4j+3][n] and D[4j..4j+3][n].
+template <class VA, class VC>
+inline VC mfma_16x16x16(int dt, VA a, VA b, VC c, int line) {
+    static_assert(sizeof(VA) == 8 && sizeof(VC) == 16, "16x16x16: 4 x 16-bit A/B, 4 x fp32 C/D");
+    XOp op{};
+    op.kind = X_MFMA;
+    op.dt = dt;
+    op.bytes = 8;
+    op.p0 = 16;  // K
+    op.line = line;
+    memcpy(op.a, &a, 8);
+    memcpy(op.b, &b, 8);
     memcpy(op.c, &c, 16);
     cross_lane(op);
     VC d;
@@ -278,6 +299,8 @@ inline void launch(const char *name, void (*k)(P...), dim3 grid, dim3 block, siz
 #define __builtin_amdgcn_mov_dpp(s, c, rm, bm, bc) ::emu::update_dpp((int)0xDEADBEEF, (s), (c), (rm), (bm), (bc), __LINE__)
 #define __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, x, y, z) ::emu::mfma_16x16x32(0, (a), (b), (c), __LINE__)
 #define __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, x, y, z) ::emu::mfma_16x16x32(1, (a), (b), (c), __LINE__)
+#define __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, x, y, z) ::emu::mfma_16x16x16(0, (a), (b), (c), __LINE__)
+#define __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, x, y, z) ::emu::mfma_16x16x16(1, (a), (b), (c), __LINE__)
 #define __builtin_amdgcn_fdot2_f32_bf16(a, b, c, clamp) ::emu::dot2(0, (a), (b), (c))
 #define __builtin_amdgcn_fdot2(a, b, c, clamp) ::emu::dot2(1, (a), (b), (c))
 #define __builtin_amdgcn_perm(a, b, s) ::emu::perm((a), (b), (s))

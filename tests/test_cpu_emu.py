@@ -66,6 +66,17 @@ SWEEP = [(15, ["generic", "mfma", "valu"]), (16, ["generic"]), (17, ["generic", 
 SWEEP_HEAD_DIMS = [0, 11, 28, 29, 36, 37]
 
 
+# sweep draws at head_dim 64 and 256 on the MFMA kernel: group 8 CSR (D 64 and 256), group 8
+# paged with one request, groups 4 and 2 paged at D 256 (the 16-token tiles)
+SWEEP_MFMA_HEAD_DIMS = [4, 16, 27, 28, 37]
+
+
+def test_mfma_head_dims_in_bounds(asan_build):
+    cases = [{"sweep": s, "kernels": ["mfma"]} for s in SWEEP_MFMA_HEAD_DIMS]
+    rc, rows, err = _run(cases)
+    _assert_clean(rc, rows, err, len(SWEEP_MFMA_HEAD_DIMS))
+
+
 def test_valu_head_dims_in_bounds(asan_build):
     cases = [{"sweep": s, "kernels": ["valu"]} for s in SWEEP_HEAD_DIMS]
     rc, rows, err = _run(cases)

@@ -54,10 +54,10 @@ def kernels_for(c, csr):
     """The kernels whose host checks accept the shape (csrc/attention.hip select_kernel)."""
     pow2 = c.page_size & (c.page_size - 1) == 0
     ks = ["generic"]
-    if c.head_dim == 128 and pow2:
+    if pow2:  # the MFMA kernel (groups <= 16) and the VALU kernel (groups <= 4) take head_dim 64, 128, 256
         ks.append("mfma")
-    if c.group_size <= 4 and pow2:  # the VALU kernel takes head_dim 64, 128 and 256
-        ks.append("valu")
+        if c.group_size <= 4:
+            ks.append("valu")
     return ks
 
 

@@ -254,7 +254,17 @@ def test_attention_kernel_selection_is_host_only():
     assert b"group <= 4" in lib.sgd_last_error()
     args.kernel = _lib.KERNELS["mfma"]
     assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "mfma"
-    args.head_dim = 64  # group 8 at head_dim 64: the MFMA kernel takes head_dim 128 only
+    for d in (64, 256):  # group 8: the MFMA kernel at every head dim
+        args.head_dim = d
+        args.k_stride[:] = [8 * d, 0, d, 1]
+        args.v_stride[:] = [8 * d, 0, d, 1]
+        assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "mfma"
+        args.kernel = _lib.KERNELS["auto"]
+        assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "mfma"
+        args.kernel = _lib.KERNELS["mfma"]
+    args.k_stride[:] = [8 * 64 + 8, 0, 64, 2]  # a dim stride of 2: the generic kernel only
+    args.v_stride[:] = [8 * 64 + 8, 0, 64, 2]
+    args.head_dim = 64
     assert lib.sgd_attention_kernel(ctypes.byref(args)) == -22
     args.kernel = _lib.KERNELS["auto"]
     assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "generic"
