@@ -172,3 +172,44 @@ def test_llama8b_32_layer_graph_shrinking_batches():
     # over capacity: the host refuses before the graph is touched
     with pytest.raises(ValueError):
         graph.update([x[0][:1] for x in fx], [x[4][:1] for x in fx], [c.max_context + 1], [1])
+
+
+@pytest.mark.parametrize("mode", [Mode.D4, Mode.R1])
+def test_graph_replay_single_split_rows_from_the_attention(mode):
+    """Batch capacity 128 x 32 query heads = 4096 merge rows, beyond one residency round
+    of the merge (8 rows per CU on 256 CUs): each request's first split writes its rows and
+    the merge only combines the multi-split ones.  Two layers under one hipGraph, batch
+    128 -> 100 -> 3 with contexts growing by one and a mix of one and several splits per
+    request; outputs, scratch and counters poisoned before every replay, so every row must
+    be rewritten by the replay; every layer of every step against the FP32 oracle."""
+    c = DecodeConfig(batch_capacity=128, max_splits=8, max_context=4096, page_size=1, workers=256)
+    base = W.lognormal_lengths(128, 384, 16, 3000, seed=31)
+    layers = 2
+    fx = [W.make_csr_inputs(c, [x + 3 for x in base], seed=90 + i, pool_tokens=sum(base) + 128 * 4)
+          for i in range(layers)]
+    engine = DecodeEngine(c, layers=layers, force_mode=mode)
+    if not engine.direct_first_split:
+        pytest.skip("this device holds all 4096 merge rows in one residency round")
+    key = PlanKey("batch", "hints", (32, 8, 128))
+    graph = DecodeGraph(engine, [key] * layers, [(x[1], x[2]) for x in fx],
+                        index_capacity=[x[4].numel() for x in fx])
+    for step, batch in enumerate([128, 100, 3]):
+        lengths = [x + step for x in base[:batch]]
+        splits = W.split_hints(lengths, c.max_splits)
+        assert 1 in splits and max(splits) > 1 or batch == 3
+        print(f"graph direct mode={mode.name} step={step} batch={batch} "
+              f"single={splits.count(1)}", flush=True)
+        indptrs, indices = _csr_step(fx, lengths)
+        graph.update([x[0][:batch] for x in fx], indices, lengths, splits)
+        if step == 0:
+            graph.capture()
+        for layer in engine.layers:
+            layer.partial.fill_(float("nan"))
+            layer.output.fill_(float("nan"))
+            layer.counter.fill_(7777)
+        outs = graph.replay()
+        torch.cuda.synchronize()
+        for i, x in enumerate(fx):
+            exp = OA.csr_attention(x[0], x[1], x[2], indptrs[i], indices[i].cuda(), lengths)
+            close(outs[i][:batch], exp[:batch], msg=f"layer {i} step {step}")
+            assert not outs[i][batch:].float().abs().sum().item()  # rows past the batch: zeros

@@ -80,3 +80,30 @@ def test_noalloc_invalid_metadata_writes_nan():
     decode_noalloc(c, q, k, v, pages, L, S, A, out)
     torch.cuda.synchronize()
     assert torch.isnan(out.float()).all()
+
+
+@pytest.mark.parametrize("mode", [Mode.D4, Mode.R1])
+def test_noalloc_single_split_rows_from_the_attention(mode):
+    """Batch capacity 128 x 32 query heads = 4096 merge rows (16.8 MB of split slots):
+    beyond one residency round of the merge on 256 CUs, so both entries let each
+    request's first split write its rows and merge only the multi-split ones.  The output
+    is poisoned, the second call is smaller: every row of both calls must be rewritten."""
+    c = DecodeConfig(batch_capacity=128, max_splits=8, max_context=4096, page_size=1, workers=256)
+    if not DecodeEngine(c).direct_first_split:
+        pytest.skip("this device holds all 4096 merge rows in one residency round")
+    out = torch.empty((c.batch_capacity, c.query_heads, c.head_dim), dtype=torch.bfloat16, device="cuda")
+    full = W.lognormal_lengths(128, 384, 16, 3000, seed=33)
+    for n, shrink in ((128, 1), (41, 2)):
+        lengths = [max(1, x // shrink) for x in full[:n]]
+        splits = W.split_hints(lengths, c.max_splits)
+        assert 1 in splits and max(splits) > 1
+        print(f"noalloc direct mode={mode.name} batch={n} single={splits.count(1)}", flush=True)
+        q, k, v, indptr, indices = W.make_csr_inputs(c, lengths, seed=80 + n, pool_tokens=1 << 17)
+        expect = _allocating(c, mode, lengths, splits, (q, k, v, indices), indptr, torch.bfloat16)
+        L, S, A = _plan_inputs(c, lengths, splits)
+        out.fill_(float("nan"))
+        got = decode_noalloc(c, q, k, v, indices, L, S, A, out, indptr=indptr, force_mode=mode)
+        torch.cuda.synchronize()
+        assert torch.equal(got, expect)
+        close(got[:n], OA.csr_attention(q, k, v, indptr, indices, lengths)[:n])
+        assert not got[n:].float().abs().sum().item()
