@@ -2,7 +2,7 @@
  * ORACLE -- test infrastructure only.
  *
  * CPU restatement of the reference's decode-plan construction and split merge,
- * used as the checker for the HIP kernels.  Only tests/, __graft_entry__.smoke()
+ * which the HIP kernels are tested against.  Only tests/, __graft_entry__.smoke()
  * and bench.py's cpu_baseline leg may load this library; the product path never
  * does.  Every function cites the reference file:line it restates (paths are
  * relative to the reference repository root).

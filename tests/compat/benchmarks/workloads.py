@@ -1,6 +1,6 @@
-"""``benchmarks.workloads`` names (reference: benchmarks/workloads.py:5-50) over this
-build's harness: the A/B/B64/uniform/holdout length sets, the split rule, the paged input
-fixture and the plan-input upload.  Input bytes come from this build's seeded generators,
+"""``benchmarks.workloads`` names (reference: benchmarks/workloads.py:5-50) over the
+package's harness: the A/B/B64/uniform/holdout length sets, the split rule, the paged input
+fixture and the plan-input upload.  Input bytes come from the package's seeded generators,
 not the reference's device RNG, so they are equal in distribution, not in value."""
 from sglang_decode import workloads as _w
 

@@ -1,8 +1,9 @@
 """The reference's GPU tests (tests/gpu/test_decode.py:12-56, tests/gpu/test_graph.py:13-51),
-restated against this build through the reference's own import paths -- the oracle as
+restated against this package through the reference's own import paths -- the oracle as
 sglang_decode.reference.attention and the harness as benchmarks.workloads (test-side
 aliases, tests/conftest.py) -- to show a caller of the reference switches without edits.
-Tolerance: BASELINE's 2e-2 abs / 1e-2 rel (tighter in rtol than the reference's 2e-2)."""
+Tolerance: 2e-2 abs / 1e-2 rel against the FP32 oracle (tighter in rtol than the
+reference's 2e-2)."""
 import pytest
 import torch
 
