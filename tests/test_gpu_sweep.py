@@ -19,7 +19,7 @@ from gpu_util import close
 
 pytestmark = pytest.mark.gpu
 
-CASES = 40
+CASES = 100
 WORK_BUDGET = 32_000 * 32 * 128  # sum(lengths) x Hq x D per case: keeps the oracle to ~1 s
 
 
