@@ -7,10 +7,10 @@
 // 16-bit dot products (v_dot2_f32_bf16 / _f16, fp32 accumulate) and wave64 DPP
 // reductions (valu_ops.h).  The kernel is HBM-bound.
 //
-// Worker = one workgroup of kWaves waves (8: two workgroups per CU, or 16: one),
-// 16 waves per CU in both cases -- the load concurrency the random 256 B row
-// gathers need, and enough waves to hide the tile math (~395 VALU instructions per
-// tile and wave, about 40% of the SIMDs' issue slots over a launch).  Tasks come from the plan's dispatch (attention_common.h); each
+// Worker = one workgroup of kWaves = 8 waves, two workgroups per CU: 16 waves per CU,
+// the load concurrency the random 256 B row gathers need, and enough waves to hide the
+// tile math (~395 VALU instructions per tile and wave, about 40% of the SIMDs' issue
+// slots over a launch).  Tasks come from the plan's dispatch (attention_common.h); each
 // task (record, kv head) is dealt to the waves in tiles of 2048 / D tokens (4 KB of K
 // and of V; tile i -> wave i % kWaves).  Per wave and tile: gather K and V rows (4 x 16
 // B loads each), stage
@@ -49,9 +49,8 @@ struct ValuShared {
 // ------------------------------------------------------------------ kernel
 template <int DT, bool CSR, int kWaves, int D, bool kOut>
 __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_args a) {
-    // 16 waves per CU (two 8-wave or one 16-wave workgroup): the load concurrency the
-    // random row gathers need to approach the HBM ceiling (4 waves per SIMD, <= 128
-    // VGPRs).
+    // 16 waves per CU (two 8-wave workgroups): the load concurrency the random row
+    // gathers need to approach the HBM ceiling (4 waves per SIMD, <= 128 VGPRs).
     extern __shared__ __align__(16) char dyn_smem[];
     using Sh = ValuShared<kWaves, D>;
     constexpr int kTile = Geo<D>::kTile, kQChunks = kHeads * D / 8, kQPerLane = (kQChunks + 63) / 64;
@@ -232,24 +231,14 @@ int launch_valu_w(const sgd_decode_args &a, hipStream_t stream) {
     return a.out ? launch_valu_o<DT, CSR, kWaves, D, true>(a, stream) : launch_valu_o<DT, CSR, kWaves, D, false>(a, stream);
 }
 
-// Waves per workgroup from the environment variable SGD_VALU_WAVES (8 or 16, default 8:
-// two workgroups per CU, the default worker count; 16 is built for head_dim 128 only).
-int valu_waves() {
-    static int w = [] {
-        const char *e = getenv("SGD_VALU_WAVES");
-        return (e && atoi(e) == 16) ? 16 : 8;
-    }();
-    return w;
-}
-
+// 8-wave workgroups, two per CU at the default worker count (one 16-wave workgroup per CU
+// measured slower: its task-end barrier idles 16 waves).
 template <int DT, bool CSR>
 int launch_valu_t(const sgd_decode_args &a, hipStream_t stream) {
     switch (a.head_dim) {
         case 64: return launch_valu_w<DT, CSR, 8, 64>(a, stream);
         case 256: return launch_valu_w<DT, CSR, 8, 256>(a, stream);
-        default:
-            return valu_waves() == 8 ? launch_valu_w<DT, CSR, 8, 128>(a, stream)
-                                     : launch_valu_w<DT, CSR, 16, 128>(a, stream);
+        default: return launch_valu_w<DT, CSR, 8, 128>(a, stream);
     }
 }
 
