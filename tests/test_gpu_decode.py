@@ -116,6 +116,31 @@ def test_noncontiguous_kv_strides():
     close(out[:2], OA.paged_attention(q, k, v, pages, lengths, c.page_size)[:2])
 
 
+@pytest.mark.parametrize("hq,kernel", [(32, "valu"), (32, "mfma"), (32, "generic"), (64, "mfma"), (64, "generic")])
+def test_views_of_packed_projection_and_fused_kv(hq, kernel):
+    """q as heads of a packed [B, (Hq + 2 Hkv) D] projection and CSR K/V as halves of one
+    [tokens, 2, Hkv, D] buffer: row strides that are not Hq D / Hkv D, unit dim strides, so
+    the tuned kernels take them (sglang_backend.py:102-103 hands the kernel such views)."""
+    c = DecodeConfig(batch_capacity=8, max_splits=8, max_context=2048, query_heads=hq, kv_heads=8, page_size=1,
+                     workers=64)
+    lengths = [1, 100, 2048, 517, 0, 64]
+    q0, k0, v0, indptr, indices = W.make_csr_inputs(c, lengths, seed=31)
+    b, d, hkv = c.batch_capacity, c.head_dim, c.kv_heads
+    qkv = torch.randn((b, (hq + 2 * hkv) * d), device="cuda", dtype=q0.dtype)
+    qkv[:, :hq * d] = q0.reshape(b, hq * d)
+    q = qkv[:, :hq * d].view(b, hq, d)
+    kv = torch.empty((k0.shape[0], 2, hkv, d), device="cuda", dtype=k0.dtype)
+    kv[:, 0].copy_(k0)
+    kv[:, 1].copy_(v0)
+    k, v = kv[:, 0], kv[:, 1]
+    assert not q.is_contiguous() and not k.is_contiguous() and k.stride(2) == 1
+    engine = DecodeEngine(c, force_mode=Mode.D1, kernel=kernel)
+    out = run(engine, lengths, (q, k, v, indices), indptr=indptr)
+    assert engine.last_kernel == kernel
+    n = len(lengths)
+    close(out[:n], OA.csr_attention(q0, k0, v0, indptr, indices, lengths)[:n])
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("hq,hkv,d", [(8, 8, 128), (16, 8, 128), (64, 8, 128), (32, 2, 128),
                                       (16, 4, 64), (16, 4, 256)])
