@@ -298,3 +298,40 @@ def test_merge_splits_min_rows_and_grid(head_dim):
     assert not full[counts == 0].float().abs().sum().item()
     assert torch.isnan(merge(2, 1).float()).all()
     assert torch.equal(merge(1, 0).view(torch.int16), full.view(torch.int16))
+
+
+def test_two_engines_on_two_streams():
+    """Separate engines may run at once (runtime/engine.py:35-37): a CSR group-4 engine and a
+    paged group-8 engine launched alternately on two streams, five rounds without a host
+    sync in between, each output against the oracle and every claim counter back at zero."""
+    c1 = DecodeConfig(batch_capacity=16, max_splits=8, max_context=4096, page_size=1, workers=512)
+    c2 = DecodeConfig(batch_capacity=8, max_splits=8, max_context=4096, query_heads=64, kv_heads=8, page_size=16,
+                      workers=512)
+    l1 = [4096, 1, 700, 2000, 33, 4000, 129, 3000]
+    l2 = [4096, 17, 1500, 999, 2048, 3]
+    q1, k1, v1, indptr, indices = W.make_csr_inputs(c1, l1, seed=41)
+    x2 = W.make_inputs(c2, l2, seed=42)
+    e1 = DecodeEngine(c1, force_mode=Mode.D1)
+    e2 = DecodeEngine(c2, force_mode=Mode.D4)
+    for e, lengths in ((e1, l1), (e2, l2)):
+        W.update_plan(e, lengths)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    outs = []
+    for _ in range(5):
+        with torch.cuda.stream(s1):
+            e1.prepare()
+            outs.append((0, e1.execute(q1, k1, v1, indices, indptr=indptr).clone()))
+        with torch.cuda.stream(s2):
+            e2.prepare()
+            outs.append((1, e2.execute(*x2).clone()))
+    torch.cuda.synchronize()
+    exp1 = OA.csr_attention(q1, k1, v1, indptr, indices, l1)
+    exp2 = OA.paged_attention(*x2[:3], x2[3], l2, c2.page_size)
+    for which, out in outs:
+        if which == 0:
+            close(out[:len(l1)], exp1[:len(l1)], msg="csr engine")
+        else:
+            close(out[:len(l2)], exp2[:len(l2)], msg="paged engine")
+    for e in (e1, e2):
+        assert not e.sync.any().item()  # claim / finished counters back at zero
