@@ -329,8 +329,10 @@ typedef struct sgd_noalloc_args {
 
 /*
  * One decode step that allocates nothing: sgd_build_plan (no policy rules, block_kv
- * 128), sgd_persistent_decode (single-split rows written straight to `out`) and
- * sgd_merge_splits_min (min_splits 2) on `stream`, with the plan and
+ * 128), sgd_persistent_decode and sgd_merge_splits_min on `stream` -- when batch_capacity
+ * x Hq exceeds one residency round of the merge (8 rows per CU) the attention writes the
+ * single-split rows straight to `out` and the merge takes min_splits 2, otherwise the
+ * merge writes every row, as DecodeEngine does -- with the plan and
  * dispatch tables, the claim counters and the split partial/LSE slots in a static
  * device array of 32 MiB held by the library on every GPU it runs on.  No counterpart
  * in the reference: for callers that cannot call hipMalloc (code under HIP graph
