@@ -69,12 +69,12 @@ int resolve_kernel(const sgd_decode_args &a) {
         case SGD_KERNEL_VALU:
             if (!valu_supported(a))
                 return einval("persistent_decode: the VALU kernel needs group <= 4, head_dim 64/128/256, unit dim "
-                              "stride, 16-byte aligned rows and a power-of-two page size");
+                              "stride and 16-byte aligned rows");
             return SGD_KERNEL_VALU;
         case SGD_KERNEL_MFMA:
             if (!mfma_supported(a))
                 return einval("persistent_decode: the MFMA kernel needs group <= 16, head_dim 64/128/256, unit dim "
-                              "stride, 16-byte aligned rows and a power-of-two page size");
+                              "stride and 16-byte aligned rows");
             return SGD_KERNEL_MFMA;
         default:
             return einval("persistent_decode: kernel %d not available", a.kernel);

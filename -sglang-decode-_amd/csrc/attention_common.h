@@ -18,6 +18,24 @@ struct TaskInfo {
     int32_t request, split, start, end, group;
 };
 
+// Token position -> (page, row within the page) of a paged layout: shift and mask when
+// the page size is a power of two (kPow2), an exact unsigned division otherwise.  Token
+// positions are never negative.
+template <bool kPow2>
+struct PageMap {
+    int32_t shift, mask, size;
+    __device__ __forceinline__ explicit PageMap(int32_t page_size)
+        : shift(__builtin_ctz((unsigned)page_size)), mask(page_size - 1), size(page_size) {}
+    __device__ __forceinline__ int32_t page(int32_t tok) const {
+        if constexpr (kPow2) return tok >> shift;
+        else return (int32_t)((uint32_t)tok / (uint32_t)size);
+    }
+    __device__ __forceinline__ int32_t row(int32_t tok) const {
+        if constexpr (kPow2) return tok & mask;
+        else return (int32_t)((uint32_t)tok % (uint32_t)size);
+    }
+};
+
 __device__ __forceinline__ TaskInfo decode_task(const sgd_decode_args &a, int32_t task, int32_t mode) {
     TaskInfo t;
     const int32_t hkv = a.kv_heads;
@@ -166,9 +184,10 @@ __device__ __forceinline__ void clear_prefetched(Prefetched *pf) {
 // (D1/D4), the dispatch entry or the record of the next task, and the page/slot indices
 // of its first kTokens tokens (0 past its end), all into s.pf[s.next] and idx[s.next].
 // `sh_indptr` (LDS, CSR) holds kv_indptr[0 .. iptr_n).
-template <bool CSR, int kTokens>
+template <bool CSR, int kTokens, bool kPow2>
 __device__ __forceinline__ void prefetch_next(const sgd_decode_args &a, const Successor &s, int32_t (*idx)[kTokens],
-                                              int lane, int page_shift, const int32_t *sh_indptr, int32_t iptr_n) {
+                                              int lane, const PageMap<kPow2> &pm, const int32_t *sh_indptr,
+                                              int32_t iptr_n) {
     Prefetched &out = s.pf[s.next];
     int32_t nt = s.next_task, nu = -1;
     TaskInfo ni{};
@@ -205,7 +224,7 @@ __device__ __forceinline__ void prefetch_next(const sgd_decode_args &a, const Su
             int32_t v = 0;
             if (tok < ni.end) {
                 if constexpr (CSR) v = a.pages[ind0 + tok];
-                else v = a.pages[(int64_t)ni.request * a.pt_stride[0] + (int64_t)(tok >> page_shift) * a.pt_stride[1]];
+                else v = a.pages[(int64_t)ni.request * a.pt_stride[0] + (int64_t)pm.page(tok) * a.pt_stride[1]];
             }
             idx[s.next][j] = v;
         }

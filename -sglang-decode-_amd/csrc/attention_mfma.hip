@@ -118,26 +118,28 @@ struct TileRegs {
 struct Src {
     const char *kbase, *vbase;
     int64_t kp, kt, vp, vt;
-    int32_t request, ind0, start, end, page_shift, page_mask;
+    int32_t request, ind0, start, end;
 };
 
 // lane l < kTileT fetches the physical page / slot index of token tok0 + l (0 past `end`,
 // which addresses an in-bounds row).
-template <bool CSR, int D>
-__device__ __forceinline__ int32_t tile_index(const sgd_decode_args &a, const Src &t, int32_t tok0, int lane) {
+template <bool CSR, int D, bool kPow2>
+__device__ __forceinline__ int32_t tile_index(const sgd_decode_args &a, const Src &t, const PageMap<kPow2> &pm,
+                                              int32_t tok0, int lane) {
     const int32_t tok = tok0 + lane;
     int32_t v = 0;
     if (lane < MGeo<D>::kTileT && tok < t.end) {
         if constexpr (CSR) v = a.pages[t.ind0 + tok];
-        else v = a.pages[(int64_t)t.request * a.pt_stride[0] + (int64_t)(tok >> t.page_shift) * a.pt_stride[1]];
+        else v = a.pages[(int64_t)t.request * a.pt_stride[0] + (int64_t)pm.page(tok) * a.pt_stride[1]];
     }
     return v;
 }
 
 // All 16 loads are unconditional, so nothing branches between a tile's loads and
 // the compute that overlaps them.
-template <bool CSR, int D>
-__device__ __forceinline__ void tile_issue_k(const Src &t, int32_t tok0, int32_t idxv, int lane, TileRegs<D> &r) {
+template <bool CSR, int D, bool kPow2>
+__device__ __forceinline__ void tile_issue_k(const Src &t, const PageMap<kPow2> &pm, int32_t tok0, int32_t idxv,
+                                             int lane, TileRegs<D> &r) {
     using G = MGeo<D>;
     const int m = lane & 15, j = lane >> 4;
 #pragma unroll
@@ -145,15 +147,16 @@ __device__ __forceinline__ void tile_issue_k(const Src &t, int32_t tok0, int32_t
         const int tt = 16 * h + m;
         const uint32_t phys = (uint32_t)__shfl(idxv, tt, 64);
         int64_t off = (int64_t)phys * t.kp;
-        if constexpr (!CSR) off += (int64_t)((tok0 + tt) & t.page_mask) * t.kt;
+        if constexpr (!CSR) off += (int64_t)pm.row(tok0 + tt) * t.kt;
 #pragma unroll
         for (int c = 0; c < G::kChunks; ++c)
             r.k[h][c] = load_stream16(t.kbase + off + (32 * c + 8 * j) * 2);
     }
 }
 
-template <bool CSR, int D>
-__device__ __forceinline__ void tile_issue_v(const Src &t, int32_t tok0, int32_t idxv, int lane, TileRegs<D> &r) {
+template <bool CSR, int D, bool kPow2>
+__device__ __forceinline__ void tile_issue_v(const Src &t, const PageMap<kPow2> &pm, int32_t tok0, int32_t idxv,
+                                             int lane, TileRegs<D> &r) {
     using G = MGeo<D>;
     const int m = lane & 15, j = lane >> 4;
     // V: dims 8m .. 8m+7 (D = 64: 8 (m % 8) ..; D = 256: also 128 + 8m ..) of the slot tokens
@@ -163,16 +166,17 @@ __device__ __forceinline__ void tile_issue_v(const Src &t, int32_t tok0, int32_t
         const int tt = slot_token(j, s);
         const uint32_t phys = (uint32_t)__shfl(idxv, tt, 64);
         int64_t off = (int64_t)phys * t.vp + vm * 16;
-        if constexpr (!CSR) off += (int64_t)((tok0 + tt) & t.page_mask) * t.vt;
+        if constexpr (!CSR) off += (int64_t)pm.row(tok0 + tt) * t.vt;
 #pragma unroll
         for (int hv = 0; hv < (D == 256 ? 2 : 1); ++hv) r.v[hv][s] = load_stream16(t.vbase + off + hv * 256);
     }
 }
 
-template <bool CSR, int D>
-__device__ __forceinline__ void tile_issue(const Src &t, int32_t tok0, int32_t idxv, int lane, TileRegs<D> &r) {
-    tile_issue_k<CSR, D>(t, tok0, idxv, lane, r);
-    tile_issue_v<CSR, D>(t, tok0, idxv, lane, r);
+template <bool CSR, int D, bool kPow2>
+__device__ __forceinline__ void tile_issue(const Src &t, const PageMap<kPow2> &pm, int32_t tok0, int32_t idxv, int lane,
+                                           TileRegs<D> &r) {
+    tile_issue_k<CSR, D>(t, pm, tok0, idxv, lane, r);
+    tile_issue_v<CSR, D>(t, pm, tok0, idxv, lane, r);
 }
 
 template <int DT>
@@ -254,7 +258,7 @@ __device__ __forceinline__ void tile_compute(TileRegs<D> &r, const uint4 (&q)[MG
     }
 }
 
-template <int DT, bool CSR, int D, bool kOut>
+template <int DT, bool CSR, int D, bool kOut, bool kPow2>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_args a) {
     using MG = MGeo<D>;
     constexpr int kTileT = MG::kTileT;
@@ -263,7 +267,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
     const int lane0 = threadIdx.x & 63, wave = uni(threadIdx.x >> 6);
     const int32_t G = a.query_heads / a.kv_heads;
     const float scale2 = a.scale * kLog2e;
-    const int page_shift = __builtin_ctz((unsigned)a.page_size);
+    const PageMap<kPow2> pm(a.page_size);
     clear_prefetched(sh.pf);
     lds_barrier();
 
@@ -288,8 +292,6 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
         t.kt = a.k_stride[1] * 2;
         t.vp = a.v_stride[0] * 2;
         t.vt = a.v_stride[1] * 2;
-        t.page_shift = page_shift;
-        t.page_mask = a.page_size - 1;
         const int32_t ntiles = (t.end - t.start + kTileT - 1) / kTileT;
         const int32_t n0 = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
         const bool prefetched = uni(sh.pf[succ.cur].task) == task;
@@ -326,12 +328,12 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
         TileRegs<D> cur, nxt;
         int32_t tile = wave, idx_next = 0;
         if (n0 > 0) {
-            const int32_t idx0 = !prefetched              ? tile_index<CSR, D>(a, t, t.start + tile * kTileT, lane)
+            const int32_t idx0 = !prefetched              ? tile_index<CSR, D>(a, t, pm, t.start + tile * kTileT, lane)
                                  : lane < kTileT ? sh.pf_idx[succ.cur][wave * kTileT + lane]
                                                  : 0;
-            tile_issue<CSR, D>(t, t.start + tile * kTileT, idx0, lane, cur);
+            tile_issue<CSR, D>(t, pm, t.start + tile * kTileT, idx0, lane, cur);
             // indices of the wave's next tile (clamped to its last one)
-            idx_next = tile_index<CSR, D>(a, t, t.start + min(tile + kWaves, ntiles - 1) * kTileT, lane);
+            idx_next = tile_index<CSR, D>(a, t, pm, t.start + min(tile + kWaves, ntiles - 1) * kTileT, lane);
         }
         if (n0 > 0) {
             if constexpr (D == 256) {
@@ -342,13 +344,13 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
                     const bool more = e + 1 < n0;
                     const int32_t nt = tile + kWaves, idx_nt = idx_next;
                     if (more) {
-                        tile_issue_k<CSR, D>(t, t.start + nt * kTileT, idx_nt, lane, nxt);
-                        idx_next = tile_index<CSR, D>(a, t, t.start + min(nt + kWaves, ntiles - 1) * kTileT, lane);
+                        tile_issue_k<CSR, D>(t, pm, t.start + nt * kTileT, idx_nt, lane, nxt);
+                        idx_next = tile_index<CSR, D>(a, t, pm, t.start + min(nt + kWaves, ntiles - 1) * kTileT, lane);
                     }
                     tile_compute<DT, D>(cur, q, min(kTileT, t.end - (t.start + tile * kTileT)), scale2, lane,
                                         m_l, den_l, o);
                     if (!more) break;
-                    tile_issue_v<CSR, D>(t, t.start + nt * kTileT, idx_nt, lane, cur);
+                    tile_issue_v<CSR, D>(t, pm, t.start + nt * kTileT, idx_nt, lane, cur);
 #pragma unroll
                     for (int c = 0; c < MG::kChunks; ++c) cur.k[0][c] = nxt.k[0][c];
                     tile = nt;
@@ -356,8 +358,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
             } else {
                 for (int32_t e = 0; e + 1 < n0; ++e) {
                     const int32_t nt = tile + kWaves;
-                    tile_issue<CSR, D>(t, t.start + nt * kTileT, idx_next, lane, nxt);
-                    idx_next = tile_index<CSR, D>(a, t, t.start + min(nt + kWaves, ntiles - 1) * kTileT, lane);
+                    tile_issue<CSR, D>(t, pm, t.start + nt * kTileT, idx_next, lane, nxt);
+                    idx_next = tile_index<CSR, D>(a, t, pm, t.start + min(nt + kWaves, ntiles - 1) * kTileT, lane);
                     tile_compute<DT, D>(cur, q, min(kTileT, t.end - (t.start + tile * kTileT)), scale2, lane,
                                         m_l, den_l, o);
                     cur = nxt;
@@ -371,7 +373,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
         // The last wave holds the fewest tiles (round-robin deal): once they are done it
         // finds the worker's next task, so those round trips overlap the other waves'
         // last tiles; the barrier below publishes it.
-        if (wave == kWaves - 1) prefetch_next<CSR, kTileT * kWaves>(a, succ, sh.pf_idx, lane, page_shift, nullptr, 0);
+        if (wave == kWaves - 1) prefetch_next<CSR, kTileT * kWaves>(a, succ, sh.pf_idx, lane, pm, nullptr, 0);
 
         // wave state to LDS: head n = lane % 16, dims 128 hv + 32j + 8i + b (D = 64: lane
         // groups j < 2 only; the others hold copies)
@@ -419,19 +421,30 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attention_mfma(sgd_decode_ar
     }, sh.pf);
 }
 
-template <int DT, bool CSR, int D, bool kOut>
+template <int DT, bool CSR, int D, bool kOut, bool kPow2>
 int launch_mfma_o(const sgd_decode_args &a, hipStream_t stream) {
     static bool attr[kOnceDevices] = {};
     constexpr int bytes = (int)sizeof(MfmaShared<D>);
-    if (int rc = set_dynamic_lds((const void *)k_attention_mfma<DT, CSR, D, kOut>, bytes, attr, "mfma attention"))
+    if (int rc = set_dynamic_lds((const void *)k_attention_mfma<DT, CSR, D, kOut, kPow2>, bytes, attr,
+                                 "mfma attention"))
         return rc;
-    hipLaunchKernelGGL((k_attention_mfma<DT, CSR, D, kOut>), dim3(a.workers), dim3(64 * kWaves), bytes, stream, a);
+    hipLaunchKernelGGL((k_attention_mfma<DT, CSR, D, kOut, kPow2>), dim3(a.workers), dim3(64 * kWaves), bytes, stream,
+                       a);
     return launch_status("persistent_decode(mfma)");
+}
+
+// A power-of-two page (CSR's page of one token included) maps tokens by shift and mask;
+// any other page size by division, in a separate build.
+template <int DT, bool CSR, int D, bool kOut>
+int launch_mfma_p(const sgd_decode_args &a, hipStream_t stream) {
+    if (CSR || (a.page_size & (a.page_size - 1)) == 0) return launch_mfma_o<DT, CSR, D, kOut, true>(a, stream);
+    if constexpr (!CSR) return launch_mfma_o<DT, CSR, D, kOut, false>(a, stream);
+    return 0;
 }
 
 template <int DT, bool CSR, int D>
 int launch_mfma_d(const sgd_decode_args &a, hipStream_t stream) {
-    return a.out ? launch_mfma_o<DT, CSR, D, true>(a, stream) : launch_mfma_o<DT, CSR, D, false>(a, stream);
+    return a.out ? launch_mfma_p<DT, CSR, D, true>(a, stream) : launch_mfma_p<DT, CSR, D, false>(a, stream);
 }
 
 template <int DT, bool CSR>
@@ -446,13 +459,12 @@ int launch_mfma_t(const sgd_decode_args &a, hipStream_t stream) {
 }  // namespace
 
 // Any group up to 16 (the padded MFMA N), head_dim 64, 128 or 256, unit dim stride,
-// 16-byte aligned rows, power-of-two page.
+// 16-byte aligned rows, any page size.
 bool mfma_supported(const sgd_decode_args &a) {
     const int g = a.query_heads / a.kv_heads;
     if (g < 1 || g > kHeadsM || (a.head_dim != 64 && a.head_dim != 128 && a.head_dim != 256)) return false;
     if (a.k_stride[3] != 1 || a.v_stride[3] != 1) return false;
     if ((reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.v)) & 15) return false;
-    if (a.page_size & (a.page_size - 1)) return false;
     for (int i = 0; i < 3; ++i)
         if (a.k_stride[i] % 8 || a.v_stride[i] % 8) return false;
     return a.k_stride[0] < (1ll << 40) && a.v_stride[0] < (1ll << 40);

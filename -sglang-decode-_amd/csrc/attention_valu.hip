@@ -47,7 +47,7 @@ struct ValuShared {
 };
 
 // ------------------------------------------------------------------ kernel
-template <int DT, bool CSR, int kWaves, int D, bool kOut>
+template <int DT, bool CSR, int kWaves, int D, bool kOut, bool kPow2>
 __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_args a) {
     // 16 waves per CU (two 8-wave workgroups): the load concurrency the random row
     // gathers need to approach the HBM ceiling (4 waves per SIMD, <= 128 VGPRs).
@@ -59,8 +59,7 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
     WaveTile<D> &wt = sh.w[wave];
     const int32_t G = a.query_heads / a.kv_heads;
     const float scale2 = a.scale * kLog2e;
-    const int page_shift = __builtin_ctz((unsigned)a.page_size);  // page_size is a power of two here
-    const int32_t page_mask = a.page_size - 1;
+    const PageMap<kPow2> pm(a.page_size);
     // CSR: kv_indptr (active + 1 entries) once per launch, so a task's index base is an
     // LDS read rather than a memory round trip between its claim and its first loads.
     int32_t iptr_n = 0;
@@ -121,10 +120,10 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
                 const int row = index_row<D>(lane);
                 i0 = row >= 0 ? sh.pf_idx[succ.cur][wave * kTile + row] : 0;
             } else {
-                i0 = tile_index<CSR, D>(a, T, T.start + wave * kTile, lane, page_shift);
+                i0 = tile_index<CSR, D>(a, T, T.start + wave * kTile, lane, pm);
             }
-            tile_issue<CSR, D>(T, wave, i0, page_mask, lane, kr, vr);
-            if (n0 > 1) idx_next = tile_index<CSR, D>(a, T, T.start + (wave + kWaves) * kTile, lane, page_shift);
+            tile_issue<CSR, D>(T, wave, i0, pm, lane, kr, vr);
+            if (n0 > 1) idx_next = tile_index<CSR, D>(a, T, T.start + (wave + kWaves) * kTile, lane, pm);
         }
         lds_barrier();  // the previous task's merge is done with shared memory
         if (wave == 0) {
@@ -151,9 +150,9 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
             const int32_t tile = wave + kWaves * e;
             const int32_t nvalid = min(kTile, T.end - (T.start + tile * kTile));
             tile_stage<D>(wt, kr, vr, lane_v, nvalid);
-            if (e + 1 < n0) tile_issue<CSR, D>(T, tile + kWaves, idx_next, page_mask, lane, kr, vr);
+            if (e + 1 < n0) tile_issue<CSR, D>(T, tile + kWaves, idx_next, pm, lane, kr, vr);
             if (e + 2 < n0)
-                idx_next = tile_index<CSR, D>(a, T, T.start + (tile + 2 * kWaves) * kTile, lane, page_shift);
+                idx_next = tile_index<CSR, D>(a, T, T.start + (tile + 2 * kWaves) * kTile, lane, pm);
             wave_sync();
             tile_compute<DT, D>(wt, sh.q, nvalid, scale2, ro, m_l, den_l, acc);
         }
@@ -163,7 +162,7 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
         // the merge barrier below publishes it to for_each_task and to the next task's
         // first tile issue.
         if (wave == kWaves - 1)
-            prefetch_next<CSR, kTile * kWaves>(a, succ, sh.pf_idx, lane, page_shift, sh.indptr, iptr_n);
+            prefetch_next<CSR, kTile * kWaves>(a, succ, sh.pf_idx, lane, pm, sh.indptr, iptr_n);
         // ---- reduce within the wave, then merge the waves
         const Roles<D> ro(lane);
         float mh[kHeads], dh[kHeads];
@@ -214,21 +213,30 @@ __global__ __launch_bounds__(64 * kWaves, 4) void k_attention_valu(sgd_decode_ar
     }, sh.pf);
 }
 
-template <int DT, bool CSR, int kWaves, int D, bool kOut>
+template <int DT, bool CSR, int kWaves, int D, bool kOut, bool kPow2>
 int launch_valu_o(const sgd_decode_args &a, hipStream_t stream) {
     static bool attr[kOnceDevices] = {};
     const int bytes = (int)sizeof(ValuShared<kWaves, D>);
-    if (int rc = set_dynamic_lds((const void *)k_attention_valu<DT, CSR, kWaves, D, kOut>, bytes, attr,
+    if (int rc = set_dynamic_lds((const void *)k_attention_valu<DT, CSR, kWaves, D, kOut, kPow2>, bytes, attr,
                                  "valu attention"))
         return rc;
-    hipLaunchKernelGGL((k_attention_valu<DT, CSR, kWaves, D, kOut>), dim3(a.workers), dim3(64 * kWaves), bytes, stream,
-                       a);
+    hipLaunchKernelGGL((k_attention_valu<DT, CSR, kWaves, D, kOut, kPow2>), dim3(a.workers), dim3(64 * kWaves), bytes,
+                       stream, a);
     return launch_status("persistent_decode(valu)");
+}
+
+// A power-of-two page (CSR's page of one token included) maps tokens by shift and mask;
+// any other page size by division, in a separate build.
+template <int DT, bool CSR, int kWaves, int D, bool kOut>
+int launch_valu_p(const sgd_decode_args &a, hipStream_t stream) {
+    if (CSR || (a.page_size & (a.page_size - 1)) == 0) return launch_valu_o<DT, CSR, kWaves, D, kOut, true>(a, stream);
+    if constexpr (!CSR) return launch_valu_o<DT, CSR, kWaves, D, kOut, false>(a, stream);
+    return 0;
 }
 
 template <int DT, bool CSR, int kWaves, int D>
 int launch_valu_w(const sgd_decode_args &a, hipStream_t stream) {
-    return a.out ? launch_valu_o<DT, CSR, kWaves, D, true>(a, stream) : launch_valu_o<DT, CSR, kWaves, D, false>(a, stream);
+    return a.out ? launch_valu_p<DT, CSR, kWaves, D, true>(a, stream) : launch_valu_p<DT, CSR, kWaves, D, false>(a, stream);
 }
 
 // 8-wave workgroups, two per CU at the default worker count (one 16-wave workgroup per CU
@@ -249,7 +257,6 @@ bool valu_supported(const sgd_decode_args &a) {
     if (g > kHeads || (a.head_dim != 64 && a.head_dim != 128 && a.head_dim != 256)) return false;
     if (a.k_stride[3] != 1 || a.v_stride[3] != 1) return false;
     if ((reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.v)) & 15) return false;
-    if (a.page_size & (a.page_size - 1)) return false;
     for (int i = 0; i < 3; ++i)
         if (a.k_stride[i] % 8 || a.v_stride[i] % 8) return false;
     // 32-bit page index times the page stride must stay a valid 64-bit byte offset

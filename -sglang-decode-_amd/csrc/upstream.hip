@@ -55,6 +55,7 @@ __global__ __launch_bounds__(64 * kUpWaves, 4) void k_upstream_split(sgd_decode_
     WaveTile<kD> &wt = sh.w[wave];
     const int32_t G = a.query_heads / a.kv_heads;
     const float scale2 = a.scale * kLog2e;
+    const PageMap<true> csr_pages(1);  // CSR: one token per page (no page arithmetic)
 
     TileSrc T;
     T.request = b;
@@ -72,9 +73,9 @@ __global__ __launch_bounds__(64 * kUpWaves, 4) void k_upstream_split(sgd_decode_
     uint4 kr[kRowsLoads], vr[kRowsLoads];
     int32_t idx_next = 0;
     if (n0 > 0) {
-        const int32_t i0 = tile_index<true, kD>(a, T, T.start + wave * kTile, lane, 0);
-        tile_issue<true, kD>(T, wave, i0, 0, lane, kr, vr);
-        if (n0 > 1) idx_next = tile_index<true, kD>(a, T, T.start + (wave + kUpWaves) * kTile, lane, 0);
+        const int32_t i0 = tile_index<true, kD>(a, T, T.start + wave * kTile, lane, csr_pages);
+        tile_issue<true, kD>(T, wave, i0, csr_pages, lane, kr, vr);
+        if (n0 > 1) idx_next = tile_index<true, kD>(a, T, T.start + (wave + kUpWaves) * kTile, lane, csr_pages);
     }
     if (wave == 0) {  // q rows of the group: head lane / 16, dims 8 (lane % 16) ..; zero past G
         const int h = lane >> 4, c = lane & 15;
@@ -102,8 +103,8 @@ __global__ __launch_bounds__(64 * kUpWaves, 4) void k_upstream_split(sgd_decode_
         const int32_t tile = wave + kUpWaves * e;
         const int32_t nvalid = min(kTile, T.end - (T.start + tile * kTile));
         tile_stage<kD>(wt, kr, vr, lane, nvalid);
-        if (e + 1 < n0) tile_issue<true, kD>(T, tile + kUpWaves, idx_next, 0, lane, kr, vr);
-        if (e + 2 < n0) idx_next = tile_index<true, kD>(a, T, T.start + (tile + 2 * kUpWaves) * kTile, lane, 0);
+        if (e + 1 < n0) tile_issue<true, kD>(T, tile + kUpWaves, idx_next, csr_pages, lane, kr, vr);
+        if (e + 2 < n0) idx_next = tile_index<true, kD>(a, T, T.start + (tile + 2 * kUpWaves) * kTile, lane, csr_pages);
         wave_sync();
         tile_compute<DT, kD>(wt, sh.q, nvalid, scale2, ro, m_l, den_l, acc);
     }

@@ -149,15 +149,15 @@ __device__ __forceinline__ int index_row(int lane) {
 }
 
 // Lane 16r + j fetches the page/slot index of token tok0 + index_row(lane) (0 if none).
-template <bool CSR, int D>
+template <bool CSR, int D, bool kPow2>
 __device__ __forceinline__ int32_t tile_index(const sgd_decode_args &a, const TileSrc &t, int32_t tok0, int lane,
-                                              int page_shift) {
+                                              const PageMap<kPow2> &pm) {
     const int row = index_row<D>(lane);
     const int32_t tok = tok0 + row;
     int32_t v = 0;
     if (row >= 0 && tok < t.end) {
         if constexpr (CSR) v = a.pages[t.ind0 + tok];
-        else v = a.pages[(int64_t)t.request * a.pt_stride[0] + (int64_t)(tok >> page_shift) * a.pt_stride[1]];
+        else v = a.pages[(int64_t)t.request * a.pt_stride[0] + (int64_t)pm.page(tok) * a.pt_stride[1]];
     }
     return v;
 }
@@ -168,9 +168,9 @@ __device__ __forceinline__ int32_t tile_index(const sgd_decode_args &a, const Ti
 // exec-mask branch sits between a tile's loads and the compute they overlap: rows past
 // `end` got index 0 from tile_index, which addresses a row of page 0 (in bounds), and
 // tile_stage zeroes them.
-template <bool CSR, int D>
-__device__ __forceinline__ void tile_issue(const TileSrc &t, int32_t tile, int32_t idxv, int32_t page_mask, int lane,
-                                           uint4 (&kr)[kRowsLoads], uint4 (&vr)[kRowsLoads]) {
+template <bool CSR, int D, bool kPow2>
+__device__ __forceinline__ void tile_issue(const TileSrc &t, int32_t tile, int32_t idxv, const PageMap<kPow2> &pm,
+                                           int lane, uint4 (&kr)[kRowsLoads], uint4 (&vr)[kRowsLoads]) {
     const int c = lane % Geo<D>::kChunks;
     const int32_t tok0 = t.start + tile * Geo<D>::kTile;
 #define SGD_LOAD_ROW(I)                                                                              \
@@ -182,7 +182,7 @@ __device__ __forceinline__ void tile_issue(const TileSrc &t, int32_t tile, int32
         }                                                                                            \
         int64_t ko = (int64_t)phys * t.kp + c * 16, vo = (int64_t)phys * t.vp + c * 16;              \
         if constexpr (!CSR) {                                                                        \
-            const int32_t inner = (tok0 + load_row<D>(I, lane)) & page_mask;                         \
+            const int32_t inner = pm.row(tok0 + load_row<D>(I, lane));                               \
             ko += (int64_t)inner * t.kt;                                                             \
             vo += (int64_t)inner * t.vt;                                                             \
         }                                                                                            \

@@ -335,3 +335,21 @@ def test_two_engines_on_two_streams():
             close(out[:len(l2)], exp2[:len(l2)], msg="paged engine")
     for e in (e1, e2):
         assert not e.sync.any().item()  # claim / finished counters back at zero
+
+
+@pytest.mark.parametrize("page", [3, 12, 48])
+@pytest.mark.parametrize("hq", [32, 64])
+def test_page_sizes_not_a_power_of_two(page, hq):
+    """Pages of 3, 12 and 48 tokens on the tuned kernels (tokens mapped to (page, row) by
+    division) and the generic one, group 4 and 8, tasks and tiles crossing page ends."""
+    c = DecodeConfig(batch_capacity=6, max_splits=8, max_context=3000, query_heads=hq, kv_heads=8, page_size=page,
+                     workers=96)
+    lengths = [3000, 1, page, page + 1, 777, 0]
+    inputs = W.make_inputs(c, lengths, seed=page)
+    expected = OA.paged_attention(*inputs[:3], inputs[3], lengths, c.page_size)
+    for kernel in (["valu"] if hq == 32 else []) + ["mfma", "generic"]:
+        for mode in (Mode.D1, Mode.R1):
+            engine = DecodeEngine(c, force_mode=mode, kernel=kernel)
+            out = run(engine, lengths, inputs)
+            assert engine.last_kernel == kernel
+            close(out[:6], expected[:6], msg=f"page {page} kernel {kernel} mode {mode.name}")

@@ -51,13 +51,12 @@ def draw(seed):
 
 
 def kernels_for(c, csr):
-    """The kernels whose host checks accept the shape (csrc/attention.hip select_kernel)."""
-    pow2 = c.page_size & (c.page_size - 1) == 0
-    ks = ["generic"]
-    if pow2:  # the MFMA kernel (groups <= 16) and the VALU kernel (groups <= 4) take head_dim 64, 128, 256
-        ks.append("mfma")
-        if c.group_size <= 4:
-            ks.append("valu")
+    """The kernels whose host checks accept the shape (csrc/attention.hip select_kernel): the
+    MFMA kernel (groups <= 16) and the VALU kernel (groups <= 4) take head_dim 64, 128 and 256
+    and any page size (a power of two by shift and mask, any other by division)."""
+    ks = ["generic", "mfma"]
+    if c.group_size <= 4:
+        ks.append("valu")
     return ks
 
 

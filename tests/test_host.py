@@ -247,6 +247,17 @@ def test_attention_kernel_selection_is_host_only():
     for workers in (108, 256, 512):
         args.workers = workers
         assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "valu"
+    # paged with a page size that is not a power of two: still the tuned kernels
+    args.csr, args.page_size = 0, 12
+    args.k_stride[:] = [12 * 1024, 1024, 128, 1]
+    args.v_stride[:] = [12 * 1024, 1024, 128, 1]
+    assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "valu"
+    args.kernel = _lib.KERNELS["mfma"]
+    assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "mfma"
+    args.kernel = _lib.KERNELS["auto"]
+    args.csr, args.page_size = 1, 1
+    args.k_stride[:] = [1024, 0, 128, 1]
+    args.v_stride[:] = [1024, 0, 128, 1]
     args.query_heads = 64  # group 8: no VALU kernel, the MFMA one serves it
     assert _lib.KERNEL_NAMES[lib.sgd_attention_kernel(ctypes.byref(args))] == "mfma"
     args.kernel = _lib.KERNELS["valu"]
