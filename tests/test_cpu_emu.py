@@ -77,6 +77,17 @@ def test_mfma_head_dims_in_bounds(asan_build):
     _assert_clean(rc, rows, err, len(SWEEP_MFMA_HEAD_DIMS))
 
 
+# sweep draws with pages of 12 tokens (mapped by division): group 2 (D 128) and group 4
+# (D 256, 4096-token rows) on both tuned kernels, group 16 (D 128) on the MFMA one
+SWEEP_PAGES_NOT_POW2 = [(23, ["mfma", "valu"]), (73, ["mfma", "valu"]), (22, ["mfma"])]
+
+
+def test_pages_not_a_power_of_two_in_bounds(asan_build):
+    cases = [{"sweep": s, "kernels": k} for s, k in SWEEP_PAGES_NOT_POW2]
+    rc, rows, err = _run(cases)
+    _assert_clean(rc, rows, err, sum(len(k) for _, k in SWEEP_PAGES_NOT_POW2))
+
+
 def test_valu_head_dims_in_bounds(asan_build):
     cases = [{"sweep": s, "kernels": ["valu"]} for s in SWEEP_HEAD_DIMS]
     rc, rows, err = _run(cases)
