@@ -213,3 +213,35 @@ def test_graph_replay_single_split_rows_from_the_attention(mode):
             exp = OA.csr_attention(x[0], x[1], x[2], indptrs[i], indices[i].cuda(), lengths)
             close(outs[i][:batch], exp[:batch], msg=f"layer {i} step {step}")
             assert not outs[i][batch:].float().abs().sum().item()  # rows past the batch: zeros
+
+
+def test_graph_many_replays_random_steps():
+    """One captured two-layer step replayed 60 times, each step a fresh random batch (1-32
+    requests, contexts 1-2048, 1-8 splits each, D1 forced): no state leaks from one replay
+    into the next -- claim counters back at zero after every replay, and every sixth step's
+    outputs against the FP32 oracle."""
+    c = DecodeConfig(batch_capacity=32, max_splits=8, max_context=2048, page_size=1, workers=512)
+    layers = 2
+    full = [2048] * 32
+    fx = [W.make_csr_inputs(c, full, seed=600 + i, pool_tokens=32 * 2048) for i in range(layers)]
+    engine = DecodeEngine(c, layers=layers, force_mode=Mode.D1)
+    key = PlanKey("batch", "hints", (32, 8, 128))
+    graph = DecodeGraph(engine, [key] * layers, [(x[1], x[2]) for x in fx],
+                        index_capacity=[x[4].numel() for x in fx])
+    rng = torch.Generator().manual_seed(77)
+    for step in range(60):
+        batch = int(torch.randint(1, 33, (1,), generator=rng))
+        lengths = torch.randint(1, 2049, (batch,), generator=rng).tolist()
+        splits = torch.randint(1, 9, (batch,), generator=rng).tolist()
+        indptrs, indices = _csr_step(fx, lengths)
+        graph.update([x[0][:batch] for x in fx], indices, lengths, splits)
+        if step == 0:
+            graph.capture()
+        outs = graph.replay()
+        torch.cuda.synchronize()
+        assert not engine.sync.any().item(), step
+        if step % 6 == 0:
+            print(f"replay {step}: batch {batch}", flush=True)
+            for i, x in enumerate(fx):
+                exp = OA.csr_attention(x[0], x[1], x[2], indptrs[i], indices[i].cuda(), lengths)
+                close(outs[i][:batch], exp[:batch], msg=f"replay {step} layer {i}")
