@@ -19,7 +19,7 @@ from gpu_util import close
 
 pytestmark = pytest.mark.gpu
 
-CASES = 100
+CASES = 150
 WORK_BUDGET = 32_000 * 32 * 128  # sum(lengths) x Hq x D per case: keeps the oracle to ~1 s
 
 
