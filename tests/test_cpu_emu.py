@@ -38,11 +38,21 @@ def asan_build():
     return B.build(asan=True)
 
 
+EMU_JOBS = max(1, min(6, (os.cpu_count() or 2) - 2))  # executor processes at once
+
+
 def _run(cases, **kw):
+    """Each case in an executor process of its own, up to EMU_JOBS at a time (the cases are
+    independent); the rows come back in case order."""
+    import concurrent.futures
     import run_cases as R
-    rc, out, err = R.spawn(cases, **kw)
-    rows = [json.loads(line) for line in out.splitlines() if line.startswith("{")]
+    with concurrent.futures.ThreadPoolExecutor(min(EMU_JOBS, len(cases))) as pool:
+        results = list(pool.map(lambda case: R.spawn([case], **kw), cases))
+    rc = next((r for r, _, _ in results if r != 0), 0)
+    err = "".join(e for _, _, e in results)
+    rows = [json.loads(line) for _, out, _ in results for line in out.splitlines() if line.startswith("{")]
     return rc, rows, err
+
 
 
 def _assert_clean(rc, rows, err, expected_rows):
