@@ -437,9 +437,10 @@ int launch_mfma_o(const sgd_decode_args &a, hipStream_t stream) {
 // any other page size by division, in a separate build.
 template <int DT, bool CSR, int D, bool kOut>
 int launch_mfma_p(const sgd_decode_args &a, hipStream_t stream) {
-    if (CSR || (a.page_size & (a.page_size - 1)) == 0) return launch_mfma_o<DT, CSR, D, kOut, true>(a, stream);
-    if constexpr (!CSR) return launch_mfma_o<DT, CSR, D, kOut, false>(a, stream);
-    return 0;
+    if constexpr (CSR) return launch_mfma_o<DT, CSR, D, kOut, true>(a, stream);
+    else
+        return (a.page_size & (a.page_size - 1)) == 0 ? launch_mfma_o<DT, CSR, D, kOut, true>(a, stream)
+                                                      : launch_mfma_o<DT, CSR, D, kOut, false>(a, stream);
 }
 
 template <int DT, bool CSR, int D>

@@ -229,9 +229,10 @@ int launch_valu_o(const sgd_decode_args &a, hipStream_t stream) {
 // any other page size by division, in a separate build.
 template <int DT, bool CSR, int kWaves, int D, bool kOut>
 int launch_valu_p(const sgd_decode_args &a, hipStream_t stream) {
-    if (CSR || (a.page_size & (a.page_size - 1)) == 0) return launch_valu_o<DT, CSR, kWaves, D, kOut, true>(a, stream);
-    if constexpr (!CSR) return launch_valu_o<DT, CSR, kWaves, D, kOut, false>(a, stream);
-    return 0;
+    if constexpr (CSR) return launch_valu_o<DT, CSR, kWaves, D, kOut, true>(a, stream);
+    else
+        return (a.page_size & (a.page_size - 1)) == 0 ? launch_valu_o<DT, CSR, kWaves, D, kOut, true>(a, stream)
+                                                      : launch_valu_o<DT, CSR, kWaves, D, kOut, false>(a, stream);
 }
 
 template <int DT, bool CSR, int kWaves, int D>
